@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline: chunked causal GQA prefill, 512 queries appended
+after 4096 cached tokens, 40 q / 8 kv heads, head_dim 128, f16 Q/K/V/O, f32 accumulate.
+A step is one call of nexus_hip_attn_prefill over that batch with inputs resident in HBM.
+value = algorithmic TFLOP/s (4*hd per visible (query, key) pair per head).
+
+The other BASELINE configs are reported under "extra" with their own roofline: cold 8192
+prefill (MFMA), decode at 4096 and 61440 keys (HBM), and 4-draft speculative verify (HBM).
+Decode inputs rotate over enough K/V copies to exceed the 256 MB Infinity Cache.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only cfgN] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
+MALL_BYTES = 256 << 20
+
+METRIC = "attn prefill TFLOP/s (% MFMA peak) + decode KV GB/s (% HBM peak), 1 MI355X"
+
+CONFIGS = {
+    "cfg1": dict(kind="decode", hq=16, hkv=4, hd=128, nq=1, base=4095, n_ctx=4096, q="f32", o="f32", splits=0,
+                 desc="decode 1 token, 16q/4kv, hd128, 4096 keys, f32 Q/O, f16 KV"),
+    "cfg2": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=512, base=4096, n_ctx=4608, q="f16", o="f16",
+                 desc="chunked prefill 512 queries after 4096 cached tokens, 40q/8kv, hd128, f16 Q/K/V/O, f32 accumulate"),
+    "cfg3": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=8192, base=0, n_ctx=8192, q="f16", o="f16",
+                 desc="cold prefill 8192 tokens, 40q/8kv, hd128, f16 Q/K/V/O, f32 softmax stats"),
+    "cfg4": dict(kind="decode", hq=40, hkv=8, hd=128, nq=1, base=61439, n_ctx=61440, q="f32", o="f32", splits=64,
+                 desc="decode 1 token, 40q/8kv, hd128, 61440 keys, 64 splits, f32 LSE combine"),
+    "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
+                 desc="MTP verify 4 drafts at 32768 cached tokens, 16q/2kv, hd256, causal among drafts"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def work_of(c: dict) -> tuple[float, str]:
+    from nexus_amd import capi
+
+    if c["kind"] == "prefill":
+        return capi.prefill_flops(c["hq"], c["hd"], c["nq"], c["base"], c["n_ctx"]), "flop"
+    n_keys = min(c["base"] + c["nq"] - 1, c["n_ctx"] - 1) + 1
+    return capi.decode_bytes(c["hkv"], c["hd"], n_keys, c["hq"], c["nq"]), "byte"
+
+
+def measure(name: str, steps: int, warmup: int, graph: bool = False) -> dict:
+    import torch
+
+    from nexus_amd import capi
+
+    c = CONFIGS[name]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    qdt = torch.float16 if c["q"] == "f16" else torch.float32
+    odt = torch.float16 if c["o"] == "f16" else torch.float32
+    q = torch.randn(c["nq"], c["hq"], c["hd"], generator=g, device=dev).to(qdt)
+    kv_bytes = 2 * c["hkv"] * c["n_ctx"] * c["hd"] * 2
+    # memory-bound configs rotate over distinct K/V copies so reads come from HBM
+    n_sets = 1 if c["kind"] == "prefill" else max(2, min(64, -(-2 * MALL_BYTES // kv_bytes)))
+    kvs = []
+    for _ in range(n_sets):
+        k = torch.randn(c["hkv"], c["n_ctx"], c["hd"], generator=g, device=dev).half()
+        v = torch.randn(c["hkv"], c["n_ctx"], c["hd"], generator=g, device=dev).half()
+        kvs.append((k, v))
+    out = torch.empty(c["nq"], c["hq"], c["hd"], dtype=odt, device=dev)
+    desc = capi.make_desc(n_q_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"], n_query=c["nq"],
+                          q_base_pos=c["base"], n_ctx=c["n_ctx"],
+                          q_dtype=capi.NEXUS_DT_F16 if qdt == torch.float16 else capi.NEXUS_DT_F32,
+                          o_dtype=capi.NEXUS_DT_F16 if odt == torch.float16 else capi.NEXUS_DT_F32)
+    if c["kind"] == "decode":
+        splits = c["splits"] or capi.decode_default_splits(desc)
+        ws_bytes = capi.decode_ws_bytes(desc, splits)
+    else:
+        splits = 0
+        ws_bytes = capi.prefill_ws_bytes(desc)
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+
+    def call(i: int) -> None:
+        k, v = kvs[i % n_sets]
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        if c["kind"] == "decode":
+            capi.decode_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                            splits, stream)
+        else:
+            capi.prefill_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                             ws_bytes, stream)
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if graph:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(steps):
+                call(i)
+        gr.replay()
+        torch.cuda.synchronize()
+        s0.record()
+        gr.replay()
+        s1.record()
+    else:
+        s0.record()
+        for i in range(steps):
+            call(i)
+        s1.record()
+    s1.synchronize()
+    ms = s0.elapsed_time(s1) / steps
+    work, unit = work_of(c)
+    res = {"config": name, "desc": c["desc"], "ms": ms, "kv_sets": n_sets, "launch": "graph" if graph else "stream"}
+    if unit == "flop":
+        tf = work / (ms * 1e-3) / 1e12
+        res.update(tflops=tf, frac_mfma=tf / MFMA_F16_PEAK_TFLOPS, gflop=work / 1e9)
+    else:
+        gbs = work / (ms * 1e-3) / 1e9
+        res.update(gbs=gbs, frac_hbm=gbs / HBM_PEAK_GBS, mbytes=work / 1e6, splits=splits)
+    if c["kind"] == "prefill":
+        res["splits"] = (ws_bytes // (c["nq"] * c["hq"] * (c["hd"] + 2) * 4)) if ws_bytes else 1
+    log(f"[bench] {name}: {ms * 1e3:.1f} us/step  " +
+        (f"{res['tflops']:.1f} TFLOP/s ({100 * res['frac_mfma']:.1f}% MFMA)" if unit == "flop"
+         else f"{res['gbs']:.0f} GB/s ({100 * res['frac_hbm']:.1f}% HBM)"))
+    return res
+
+
+def cpu_baseline(target_s: float = 10.0) -> dict:
+    """The reference's CPU prefill attention (attn_batch_cpu, restated in oracle/) timed on a
+    bounded sample of the cfg2 workload: single thread (the reference's threading) plus an
+    all-cores variant."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+    from nexus_amd.inputs import make_case
+
+    c = CONFIGS["cfg2"]
+    q, k, v = make_case(n_q_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"], n_query=c["nq"],
+                        n_ctx=c["n_ctx"], seed=2024, q_f16=True)
+    n_rows_total = c["nq"] * c["hq"]
+    rng = np.random.default_rng(0)
+    order = rng.permutation(n_rows_total).astype(np.int32)
+
+    def run(rows, threads):
+        t0 = time.perf_counter()
+        O.attn_batch_rows(q, k, v, rows, n_kv_heads=c["hkv"], n_ctx=c["n_ctx"], q_base_pos=c["base"],
+                          n_threads=threads)
+        return time.perf_counter() - t0
+
+    def flops(rows):
+        keys = np.minimum(c["base"] + rows // c["hq"], c["n_ctx"] - 1) + 1
+        return float(4.0 * c["hd"] * keys.sum())
+
+    probe = order[:16]
+    per_row = run(probe, 1) / len(probe)
+    n = int(min(n_rows_total, max(16, target_s / max(per_row, 1e-6))))
+    rows = order[:n]
+    t1 = run(rows, 1)
+    threads = min(16, os.cpu_count() or 1)
+    rows_mt = order[: min(n_rows_total, n * threads // 2)]
+    tm = run(rows_mt, threads)
+    try:
+        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:
+        cpu_model = "unknown"
+    return {
+        "value": flops(rows) / t1 / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{n} of {n_rows_total} (query, head) rows of cfg2 drawn uniformly, single thread "
+                  f"({t1:.1f} s), oracle/attn_oracle.c restating transformer.h:8653-8685",
+        "all_cores": {"value": flops(rows_mt) / tm / 1e12, "cores": threads, "rows": int(len(rows_mt)),
+                      "seconds": tm},
+        "cpu_model": cpu_model,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=sorted(CONFIGS), default=None,
+                    help="measure one config only (for profiling runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build's attention path runs on a single MI355X "
+              "(multi-GPU sharding is design-only, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from nexus_amd import capi
+
+    capi.load()
+    props = torch.cuda.get_device_properties(0)
+    log(f"[bench] device {props.name} CUs={props.multi_processor_count} lib={capi.version()}")
+
+    if args.only:
+        measure(args.only, args.steps, args.warmup)
+        return 0
+
+    head = measure("cfg2", args.steps, args.warmup)
+    extra = {}
+    for name in ("cfg3", "cfg4", "cfg1", "cfg5"):
+        steps = max(5, args.steps // 5) if name == "cfg3" else args.steps
+        extra[name] = measure(name, steps, args.warmup)
+    extra["cfg1_graph"] = measure("cfg1", args.steps, args.warmup, graph=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle, bounded sample) ...")
+        cpu = cpu_baseline()
+        log(f"[bench] CPU baseline: {cpu['value'] * 1e3:.2f} GFLOP/s single thread")
+
+    c2 = CONFIGS["cfg2"]
+    line = {
+        "metric": METRIC,
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1), torch RNG on device)",
+        "config": {"workload": "cfg2: " + c2["desc"], "n_q_heads": c2["hq"], "n_kv_heads": c2["hkv"],
+                   "head_dim": c2["hd"], "n_query": c2["nq"], "q_base_pos": c2["base"], "n_ctx": c2["n_ctx"],
+                   "kv_splits": head["splits"], "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": head["tflops"] / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "prefill_kernel<128,f16,f16> + combine_kernel (whole call timed)",
+                     "algorithmic_gflop_per_call": head["gflop"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+        "device": {"name": props.name, "cus": props.multi_processor_count},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

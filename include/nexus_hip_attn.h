@@ -1,0 +1,115 @@
+/*
+ * nexus_hip_attn.h -- C ABI of the MI355X (gfx950) attention kernels.
+ *
+ * This is the drop-in boundary for Nexus's attention operator.  The reference engine
+ * calls its GPU attention through VulkanBackend member functions that take host
+ * pointers and return `false` (before any side effect) when they cannot run:
+ *   attention_flash_gpu   src/gpu/vulkan_backend.h:604-608 (impl :4260-4408)
+ *   attention_batch_gpu   src/gpu/vulkan_backend.h:584-588 (impl :3819-3934)
+ *   attention_stream_gpu  src/gpu/vulkan_backend.h:594-599 (impl :4085-4257)
+ *   attention_gpu         src/gpu/vulkan_backend.h:576-580 (impl :3731-3817)
+ *   q35_full_layer's attention core (split-K part + comb over the device KV mirror)
+ *                         src/gpu/vulkan_backend.h:5272-5483,
+ *                         src/gpu/shaders/qwen35_attn_part.comp, qwen35_attn_comb.comp
+ * The C++ backend in nexus_amd/host/hip_attn_backend.h keeps those member signatures and
+ * calls the two entry points below with device pointers.  All calls are asynchronous
+ * on the given stream; the library allocates nothing on these paths.
+ *
+ * Layouts (identical to the reference):
+ *   Q    [n_query][n_q_heads][head_dim]           f32 or f16 (q_dtype)
+ *   K, V [n_kv_heads][kv_row_stride][head_dim]    f16 bit patterns (uint16)
+ *        kv_row_stride = n_ctx for the packed layout of KVCache::pack_k/pack_v
+ *        (src/model/kvcache.h:655-672), = slot capacity for the device mirror
+ *        [kv_head][cap][hd] (src/gpu/vulkan_backend.h:488, 5411)
+ *   Out  [n_query][n_q_heads][head_dim]           f32 or f16 (o_dtype)
+ *   GQA: q head h reads kv head h * n_kv_heads / n_q_heads (attn_flash.comp:55)
+ *   Mask: query i sits at absolute position q_base_pos + i and sees keys
+ *         [start, min(q_base_pos + i, n_ctx - 1)], start = q_pos + 1 - sliding_window
+ *         when sliding_window > 0 (transformer.h:8666-8670); a query that sees no key
+ *         writes zeros (transformer.h:8682).
+ *   Scores: s = (q.k) * scale, then softcap * tanh(s / softcap) when softcap > 0.
+ *
+ * Errors: every entry point validates its arguments first and returns a negative
+ * code WITHOUT launching anything or touching any output when it declines; the C++
+ * wrapper maps that to the reference's `return false` (caller uses the CPU path).
+ */
+#ifndef NEXUS_HIP_ATTN_H
+#define NEXUS_HIP_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers (it is `struct ihipStream_t*`). */
+typedef struct ihipStream_t* nexus_stream_t;
+
+enum nexus_dtype {
+    NEXUS_DT_F32 = 0,
+    NEXUS_DT_F16 = 1
+};
+
+enum nexus_status {
+    NEXUS_OK              = 0,
+    NEXUS_E_UNSUPPORTED   = -1,   /* shape the kernels do not cover (declined, like nx_decline) */
+    NEXUS_E_INVALID       = -2,   /* null pointer or inconsistent argument */
+    NEXUS_E_WORKSPACE     = -3,   /* workspace missing or too small for the requested split */
+    NEXUS_E_LAUNCH        = -4    /* the HIP runtime refused the launch */
+};
+
+/* One attention call.  Mirrors the push constants of attn_flash.comp:18-31
+ * {Hq, Hkv, hd, n_ctx, n_query, q_base_pos, sliding_window, scale, softcap}
+ * plus the row stride of the cache and the Q/O element types. */
+typedef struct nexus_attn_desc {
+    int32_t n_q_heads;       /* Hq  (> 0, multiple of n_kv_heads)                    */
+    int32_t n_kv_heads;      /* Hkv (> 0)                                            */
+    int32_t head_dim;        /* 64, 128 or 256 (reference: hd % 64 == 0, hd <= 256) */
+    int32_t n_query;         /* queries in this call (> 0)                           */
+    int32_t q_base_pos;      /* absolute position of query 0 (>= 0)                  */
+    int32_t n_ctx;           /* keys [0, n_ctx) are valid in K/V (> 0)               */
+    int64_t kv_row_stride;   /* tokens between kv heads in K/V (>= n_ctx)            */
+    int32_t sliding_window;  /* 0 = off                                              */
+    float   scale;           /* 0 = 1/sqrt(head_dim)                                 */
+    float   softcap;         /* 0 = off                                              */
+    int32_t q_dtype;         /* enum nexus_dtype                                     */
+    int32_t o_dtype;         /* enum nexus_dtype                                     */
+} nexus_attn_desc;
+
+/* Causal GQA flash-attention prefill over an f16 cache: cold prompts (q_base_pos = 0)
+ * and prompt chunks appended after q_base_pos cached tokens.  Replaces
+ * attention_flash_gpu / attention_batch_gpu / attention_stream_gpu
+ * (src/gpu/vulkan_backend.h:584-608).  The workspace holds split-KV partials; pass
+ * NULL/0 to run unsplit.  nexus_hip_attn_prefill_ws_bytes() returns the size that
+ * enables the split the library would choose for this shape on this device. */
+int nexus_hip_attn_prefill(const nexus_attn_desc* desc,
+                           const void* q, const uint16_t* k, const uint16_t* v, void* out,
+                           void* workspace, size_t workspace_bytes,
+                           nexus_stream_t stream);
+size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc);
+
+/* Split-KV decode over the cache: n_query >= 1 tokens at positions q_base_pos + i
+ * (n_query = 1 is ordinary decode, n_query > 1 is speculative/MTP verify with the
+ * causal mask among the drafts).  Replaces attention_gpu (vulkan_backend.h:576-580)
+ * and the attention core of q35_full_layer (part + comb, vulkan_backend.h:5462-5482).
+ * partial_ws is f32 [n_query * n_q_heads][n_splits][head_dim + 2] holding, per split,
+ * (sum_k e^{s_k - m} v_k, m, l) exactly as qwen35_attn_part.comp:3 defines them;
+ * n_splits <= 0 lets the library choose.  Size from nexus_hip_attn_decode_ws_bytes(). */
+int nexus_hip_attn_decode(const nexus_attn_desc* desc,
+                          const void* q, const uint16_t* k, const uint16_t* v, void* out,
+                          float* partial_ws, int n_splits,
+                          nexus_stream_t stream);
+size_t nexus_hip_attn_decode_ws_bytes(const nexus_attn_desc* desc, int n_splits);
+/* The split count nexus_hip_attn_decode uses when called with n_splits <= 0. */
+int nexus_hip_attn_decode_default_splits(const nexus_attn_desc* desc);
+
+/* Message for the last non-zero status on the calling thread ("" if none). */
+const char* nexus_hip_attn_last_error(void);
+/* Library version, e.g. "nexus_hip_attn 0.1.0 gfx950". */
+const char* nexus_hip_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NEXUS_HIP_ATTN_H */

@@ -1,0 +1,164 @@
+"""ctypes binding of the C ABI in include/nexus_hip_attn.h.
+
+This is the Python side of the drop-in boundary: it loads the in-tree
+libnexus_hip_attn.so and exposes the two entry points with device pointers.  There is
+no fallback: if the library is missing, or a call is declined, an exception is raised.
+torch is only used (in nexus_amd.ops) to own device memory and the stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libnexus_hip_attn.so"
+
+NEXUS_DT_F32 = 0
+NEXUS_DT_F16 = 1
+
+NEXUS_OK = 0
+NEXUS_E_UNSUPPORTED = -1
+NEXUS_E_INVALID = -2
+NEXUS_E_WORKSPACE = -3
+NEXUS_E_LAUNCH = -4
+
+# Every symbol include/nexus_hip_attn.h declares (checked by tests/test_capi.py).
+EXPORTED_SYMBOLS = (
+    "nexus_hip_attn_prefill",
+    "nexus_hip_attn_prefill_ws_bytes",
+    "nexus_hip_attn_decode",
+    "nexus_hip_attn_decode_ws_bytes",
+    "nexus_hip_attn_decode_default_splits",
+    "nexus_hip_attn_last_error",
+    "nexus_hip_attn_version",
+)
+
+
+class AttnDesc(ctypes.Structure):
+    """struct nexus_attn_desc (include/nexus_hip_attn.h)."""
+
+    _fields_ = [
+        ("n_q_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("n_query", ctypes.c_int32),
+        ("q_base_pos", ctypes.c_int32),
+        ("n_ctx", ctypes.c_int32),
+        ("kv_row_stride", ctypes.c_int64),
+        ("sliding_window", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("softcap", ctypes.c_float),
+        ("q_dtype", ctypes.c_int32),
+        ("o_dtype", ctypes.c_int32),
+    ]
+
+
+def make_desc(*, n_q_heads: int, n_kv_heads: int, head_dim: int, n_query: int, q_base_pos: int,
+              n_ctx: int, kv_row_stride: int | None = None, sliding_window: int = 0,
+              scale: float = 0.0, softcap: float = 0.0, q_dtype: int = NEXUS_DT_F32,
+              o_dtype: int = NEXUS_DT_F32) -> AttnDesc:
+    return AttnDesc(n_q_heads, n_kv_heads, head_dim, n_query, q_base_pos, n_ctx,
+                    n_ctx if kv_row_stride is None else kv_row_stride, sliding_window,
+                    scale, softcap, q_dtype, o_dtype)
+
+
+class NexusAttnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"nexus_hip_attn status {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load the native library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"native library {p} is missing: run __graft_entry__.build() "
+                           "(python -m nexus_amd.build) first")
+    lib = ctypes.CDLL(str(p))
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    dp = ctypes.POINTER(AttnDesc)
+    lib.nexus_hip_attn_prefill.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
+    lib.nexus_hip_attn_prefill.restype = ctypes.c_int
+    lib.nexus_hip_attn_prefill_ws_bytes.argtypes = [dp]
+    lib.nexus_hip_attn_prefill_ws_bytes.restype = sz
+    lib.nexus_hip_attn_decode.argtypes = [dp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
+    lib.nexus_hip_attn_decode.restype = ctypes.c_int
+    lib.nexus_hip_attn_decode_ws_bytes.argtypes = [dp, ctypes.c_int]
+    lib.nexus_hip_attn_decode_ws_bytes.restype = sz
+    lib.nexus_hip_attn_decode_default_splits.argtypes = [dp]
+    lib.nexus_hip_attn_decode_default_splits.restype = ctypes.c_int
+    lib.nexus_hip_attn_last_error.argtypes = []
+    lib.nexus_hip_attn_last_error.restype = ctypes.c_char_p
+    lib.nexus_hip_attn_version.argtypes = []
+    lib.nexus_hip_attn_version.restype = ctypes.c_char_p
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().nexus_hip_attn_last_error().decode()
+
+
+def version() -> str:
+    return load().nexus_hip_attn_version().decode()
+
+
+def _check(rc: int) -> int:
+    if rc != NEXUS_OK:
+        raise NexusAttnError(rc, last_error())
+    return rc
+
+
+def prefill_ws_bytes(desc: AttnDesc) -> int:
+    return int(load().nexus_hip_attn_prefill_ws_bytes(ctypes.byref(desc)))
+
+
+def decode_ws_bytes(desc: AttnDesc, n_splits: int = 0) -> int:
+    return int(load().nexus_hip_attn_decode_ws_bytes(ctypes.byref(desc), int(n_splits)))
+
+
+def decode_default_splits(desc: AttnDesc) -> int:
+    return int(load().nexus_hip_attn_decode_default_splits(ctypes.byref(desc)))
+
+
+def prefill_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, ws: int, ws_bytes: int,
+                stream: int, check: bool = True) -> int:
+    rc = load().nexus_hip_attn_prefill(ctypes.byref(desc), q, k, v, out, ws, ws_bytes, stream)
+    return _check(rc) if check else rc
+
+
+def decode_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, ws: int, n_splits: int,
+               stream: int, check: bool = True) -> int:
+    rc = load().nexus_hip_attn_decode(ctypes.byref(desc), q, k, v, out, ws, int(n_splits), stream)
+    return _check(rc) if check else rc
+
+
+def prefill_flops(n_q_heads: int, head_dim: int, n_query: int, q_base_pos: int, n_ctx: int,
+                  sliding_window: int = 0) -> float:
+    """Algorithmic FLOPs of a causal prefill: 4*hd per visible (query, key) pair per head."""
+    pairs = 0
+    for i in range(n_query):
+        qpos = q_base_pos + i
+        last = min(qpos, n_ctx - 1)
+        start = qpos + 1 - sliding_window if (sliding_window > 0 and qpos + 1 > sliding_window) else 0
+        pairs += max(0, last - start + 1)
+    return 4.0 * head_dim * n_q_heads * pairs
+
+
+def decode_bytes(n_kv_heads: int, head_dim: int, n_keys: int, n_q_heads: int, n_query: int,
+                 q_bytes: int = 4, o_bytes: int = 4) -> float:
+    """Algorithmic HBM bytes of a decode: K and V of every visible key once, plus Q and O."""
+    return (2.0 * n_kv_heads * n_keys * head_dim * 2
+            + n_query * n_q_heads * head_dim * (q_bytes + o_bytes))
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,305 @@
+// nexus_amd/csrc/attn_capi.cpp -- the C ABI declared in include/nexus_hip_attn.h.
+//
+// Every entry point validates the whole call before it launches anything, so a
+// declined call (negative status) leaves every output untouched -- the contract of the
+// reference's GPU attention ops, which `return false` before any side effect
+// (src/gpu/vulkan_backend.h:4267-4277 for attention_flash_gpu, :5290-5308 for the
+// decode split-K; nx_decline :187-192).
+#include "nexus_hip_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "attn_kernels.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok()
+{
+    g_last_error[0] = '\0';
+    return NEXUS_OK;
+}
+
+constexpr int kMaxDevices = 64;
+constexpr int kMaxSplits = 1024;          // LSE combine holds one weight per split in LDS
+
+// Compute units of the current device (cached); 256 (MI355X) when no device is visible,
+// so workspace sizing is still defined on a host without a GPU.
+int device_cus()
+{
+    static int cache[kMaxDevices] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (cache[dev] > 0) return cache[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    cache[dev] = cus;
+    return cus;
+}
+
+bool supported_head_dim(int hd) { return hd == 64 || hd == 128 || hd == 192 || hd == 256; }
+
+// Shape checks shared by both entry points (pointer checks are separate so that the
+// sizing helpers can reuse this).  Mirrors the reference's declines: head_dim % 64 != 0
+// or > 256, Hq % Hkv != 0, non-positive sizes (vulkan_backend.h:4270-4273).
+int check_desc(const nexus_attn_desc* d)
+{
+    if (!d) return fail(NEXUS_E_INVALID, "desc is NULL");
+    if (d->n_q_heads <= 0 || d->n_kv_heads <= 0 || d->n_q_heads % d->n_kv_heads != 0)
+        return fail(NEXUS_E_UNSUPPORTED, "n_q_heads=%d must be a positive multiple of n_kv_heads=%d",
+                    d->n_q_heads, d->n_kv_heads);
+    if (!supported_head_dim(d->head_dim))
+        return fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in {64,128,192,256}", d->head_dim);
+    if (d->n_query <= 0 || d->n_ctx <= 0 || d->q_base_pos < 0)
+        return fail(NEXUS_E_INVALID, "n_query=%d n_ctx=%d q_base_pos=%d", d->n_query, d->n_ctx, d->q_base_pos);
+    if ((long long)d->q_base_pos + d->n_query > INT_MAX - 4096 || d->n_ctx > INT_MAX - 4096)
+        return fail(NEXUS_E_UNSUPPORTED, "positions exceed the 31-bit range");
+    if (d->kv_row_stride < d->n_ctx)
+        return fail(NEXUS_E_INVALID, "kv_row_stride=%lld < n_ctx=%d", (long long)d->kv_row_stride, d->n_ctx);
+    if (d->sliding_window < 0) return fail(NEXUS_E_INVALID, "sliding_window=%d", d->sliding_window);
+    if (!(d->scale >= 0.f) || !std::isfinite(d->scale)) return fail(NEXUS_E_INVALID, "scale=%g", (double)d->scale);
+    if (!(d->softcap >= 0.f) || !std::isfinite(d->softcap)) return fail(NEXUS_E_INVALID, "softcap=%g", (double)d->softcap);
+    if ((d->q_dtype != NEXUS_DT_F32 && d->q_dtype != NEXUS_DT_F16) ||
+        (d->o_dtype != NEXUS_DT_F32 && d->o_dtype != NEXUS_DT_F16))
+        return fail(NEXUS_E_UNSUPPORTED, "q_dtype=%d o_dtype=%d", d->q_dtype, d->o_dtype);
+    return NEXUS_OK;
+}
+
+float eff_scale(const nexus_attn_desc* d)
+{
+    return d->scale > 0.f ? d->scale : 1.0f / std::sqrt((float)d->head_dim);
+}
+
+bool is_ext(const nexus_attn_desc* d) { return d->sliding_window > 0 || d->softcap > 0.f; }
+
+// Key range any query of the call can see: [k_begin, k_end).
+void key_range(const nexus_attn_desc* d, int* k_begin, int* k_end)
+{
+    const long long last = std::min<long long>((long long)d->q_base_pos + d->n_query - 1, (long long)d->n_ctx - 1);
+    long long b = 0;
+    if (d->sliding_window > 0 && (long long)d->q_base_pos + 1 > d->sliding_window)
+        b = (long long)d->q_base_pos + 1 - d->sliding_window;
+    const long long e = last + 1;
+    if (b > e) b = e;
+    *k_begin = (int)b;
+    *k_end = (int)e;
+}
+
+int decode_rowgroups(const nexus_attn_desc* d)
+{
+    const long long rows = (long long)d->n_query * (d->n_q_heads / d->n_kv_heads);
+    return (int)((rows + nxa::kDecodeRows - 1) / nxa::kDecodeRows);
+}
+
+int default_decode_splits(const nexus_attn_desc* d)
+{
+    int kb, ke;
+    key_range(d, &kb, &ke);
+    const long long kv_len = ke - kb;
+    const long long base = (long long)d->n_kv_heads * decode_rowgroups(d);
+    const long long target = 2LL * device_cus();
+    long long s = target / base;
+    if (s < 1) s = 1;
+    const long long by_len = (kv_len + 127) / 128;           // keep >= 128 keys per split
+    if (s > by_len) s = by_len;
+    if (s < 1) s = 1;
+    if (s > kMaxSplits) s = kMaxSplits;
+    return (int)s;
+}
+
+size_t decode_ws_bytes(const nexus_attn_desc* d, int n_splits)
+{
+    return (size_t)d->n_query * (size_t)d->n_q_heads * (size_t)n_splits * (size_t)(d->head_dim + 2) * sizeof(float);
+}
+
+// Split count of the prefill kernel: enough (query block, head, split) workgroups to fill
+// two per CU (one for head_dim 256), each split keeping >= 4 key tiles.
+int prefill_splits(const nexus_attn_desc* d)
+{
+    const long long qblocks = (d->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
+    const long long base = qblocks * d->n_q_heads;
+    const long long target = (long long)(d->head_dim <= 128 ? 2 : 1) * device_cus();
+    if (base >= target) return 1;
+    long long s = target / base;
+    int kb, ke;
+    key_range(d, &kb, &ke);
+    const long long tiles = (ke - kb + nxa::kPrefillBN - 1) / nxa::kPrefillBN;
+    if (s > tiles / 4) s = tiles / 4;
+    if (s > 16) s = 16;
+    return s < 1 ? 1 : (int)s;
+}
+
+bool small_query_path(const nexus_attn_desc* d)
+{
+    return (long long)d->n_query * (d->n_q_heads / d->n_kv_heads) <= nxa::kDecodeRows;
+}
+
+int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const uint16_t* v, void* out,
+               float* part, int n_splits, hipStream_t stream)
+{
+    int kb, ke;
+    key_range(d, &kb, &ke);
+    const long long kv_len = ke - kb;
+    long long chunk = (kv_len + n_splits - 1) / n_splits;
+    chunk = (chunk + nxa::kDecodeKeys - 1) / nxa::kDecodeKeys * nxa::kDecodeKeys;
+    if (chunk < nxa::kDecodeKeys) chunk = nxa::kDecodeKeys;
+
+    nxa::DecodeArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.part = part;
+    a.kv_stride = d->kv_row_stride;
+    a.n_q_heads = d->n_q_heads;
+    a.n_kv_heads = d->n_kv_heads;
+    a.group = d->n_q_heads / d->n_kv_heads;
+    a.n_query = d->n_query;
+    a.q_base = d->q_base_pos;
+    a.n_ctx = d->n_ctx;
+    a.sliding_window = d->sliding_window;
+    a.scale = eff_scale(d);
+    a.scale_log2 = a.scale * 1.4426950408889634f;
+    a.softcap = d->softcap;
+    a.n_splits = n_splits;
+    a.chunk = (int)chunk;
+    a.k_begin = kb;
+    a.k_end = ke;
+    a.n_rows = d->n_query * a.group;
+    hipError_t e = nxa::launch_decode(a, d->head_dim, d->q_dtype == NEXUS_DT_F32, is_ext(d),
+                                      decode_rowgroups(d), stream);
+    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
+    nxa::CombineArgs c{};
+    c.part = part;
+    c.out = out;
+    c.n_rows = d->n_query * d->n_q_heads;
+    c.n_splits = n_splits;
+    e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
+    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nexus_hip_attn_decode_ws_bytes(const nexus_attn_desc* desc, int n_splits)
+{
+    if (check_desc(desc) != NEXUS_OK) return 0;
+    if (n_splits <= 0) n_splits = default_decode_splits(desc);
+    if (n_splits > kMaxSplits) return 0;
+    return decode_ws_bytes(desc, n_splits);
+}
+
+int nexus_hip_attn_decode_default_splits(const nexus_attn_desc* desc)
+{
+    if (check_desc(desc) != NEXUS_OK) return 0;
+    return default_decode_splits(desc);
+}
+
+int nexus_hip_attn_decode(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
+                          const uint16_t* v, void* out, float* partial_ws, int n_splits,
+                          nexus_stream_t stream)
+{
+    const int rc = check_desc(desc);
+    if (rc != NEXUS_OK) return rc;
+    if (!q || !k || !v || !out) return fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
+    if (!partial_ws) return fail(NEXUS_E_WORKSPACE, "partial_ws is NULL");
+    if (n_splits <= 0) n_splits = default_decode_splits(desc);
+    if (n_splits > kMaxSplits) return fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
+    return run_decode(desc, q, k, v, out, partial_ws, n_splits, (hipStream_t)stream);
+}
+
+size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
+{
+    if (check_desc(desc) != NEXUS_OK) return 0;
+    if (small_query_path(desc)) return decode_ws_bytes(desc, default_decode_splits(desc));
+    const int s = prefill_splits(desc);
+    if (s <= 1) return 0;
+    return (size_t)desc->n_query * (size_t)desc->n_q_heads * (size_t)s * (size_t)(desc->head_dim + 2) * sizeof(float);
+}
+
+int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
+                           const uint16_t* v, void* out, void* workspace, size_t workspace_bytes,
+                           nexus_stream_t stream)
+{
+    const int rc = check_desc(desc);
+    if (rc != NEXUS_OK) return rc;
+    if (!q || !k || !v || !out) return fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
+    hipStream_t s = (hipStream_t)stream;
+
+    // A handful of queries (speculative verify, tiny prompts): the split-KV kernel fills
+    // the GPU where 128-query blocks could not.
+    if (small_query_path(desc) && workspace) {
+        const int splits = default_decode_splits(desc);
+        if (workspace_bytes >= decode_ws_bytes(desc, splits))
+            return run_decode(desc, q, k, v, out, (float*)workspace, splits, s);
+    }
+
+    int splits = prefill_splits(desc);
+    const size_t need = (size_t)desc->n_query * (size_t)desc->n_q_heads * (size_t)splits *
+                        (size_t)(desc->head_dim + 2) * sizeof(float);
+    if (splits > 1 && (!workspace || workspace_bytes < need)) splits = 1;
+
+    nxa::PrefillArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.part = (float*)workspace;
+    a.kv_stride = desc->kv_row_stride;
+    a.n_q_heads = desc->n_q_heads;
+    a.n_kv_heads = desc->n_kv_heads;
+    a.group = desc->n_q_heads / desc->n_kv_heads;
+    a.n_query = desc->n_query;
+    a.q_base = desc->q_base_pos;
+    a.n_ctx = desc->n_ctx;
+    a.sliding_window = desc->sliding_window;
+    a.scale = eff_scale(desc);
+    a.scale_log2 = a.scale * 1.4426950408889634f;
+    a.softcap = desc->softcap;
+    a.n_qblocks = (desc->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
+    a.n_splits = splits;
+    const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
+    if (items > INT_MAX) return fail(NEXUS_E_UNSUPPORTED, "grid too large");
+    a.n_items = (int)items;
+    hipError_t e = nxa::launch_prefill(a, desc->head_dim, desc->q_dtype == NEXUS_DT_F32,
+                                       desc->o_dtype == NEXUS_DT_F32, is_ext(desc), s);
+    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
+    if (splits > 1) {
+        nxa::CombineArgs c{};
+        c.part = (const float*)workspace;
+        c.out = out;
+        c.n_rows = desc->n_query * desc->n_q_heads;
+        c.n_splits = splits;
+        e = nxa::launch_combine(c, desc->head_dim, desc->o_dtype == NEXUS_DT_F32, s);
+        if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
+    }
+    return ok();
+}
+
+const char* nexus_hip_attn_last_error(void) { return g_last_error; }
+
+const char* nexus_hip_attn_version(void) { return "nexus_hip_attn 0.1.0 gfx950"; }
+
+}  // extern "C"

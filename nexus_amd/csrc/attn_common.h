@@ -1,0 +1,84 @@
+// nexus_amd/csrc/attn_common.h -- device-side types and helpers shared by the gfx950
+// attention kernels (prefill MFMA kernel, split-KV decode kernel, LSE combine).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nxa {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Initial running max of the online softmax (transformer.h:8675 uses -1e30 too): finite,
+// so exp2(m_old - m_new) never evaluates (-inf) - (-inf).
+constexpr float kNegBig = -1e30f;
+// Lazy rescale threshold in log2 units: the prefill kernel keeps a stale row max until
+// the true max exceeds it by more than this, so probabilities stay <= 2^8 (safe in f16).
+constexpr float kRescaleThresh = 8.0f;
+
+// D = A(32x16) * B(16x32) + C, f16 inputs, f32 accumulate (v_mfma_f32_32x32x16_f16).
+// Lane l supplies A row (l & 31) and B column (l & 31), each with the 8 k-values of
+// k-group (l >> 5).  D: lane l holds column (l & 31), rows 8*(i/4) + 4*(l>>5) + (i&3).
+__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(u32x4 x) { return __builtin_bit_cast(f16x8, x); }
+__device__ __forceinline__ u32x4 as_u32x4(f16x8 x) { return __builtin_bit_cast(u32x4, x); }
+
+// Round-to-nearest-even f32 -> f16 of 8 values (v_cvt_pk_f16_f32 on gfx950).
+__device__ __forceinline__ f16x8 cvt_f16x8(float a0, float a1, float a2, float a3,
+                                           float a4, float a5, float a6, float a7)
+{
+    f32x2 p0 = {a0, a1}, p1 = {a2, a3}, p2 = {a4, a5}, p3 = {a6, a7};
+    f16x2 h0 = __builtin_convertvector(p0, f16x2);
+    f16x2 h1 = __builtin_convertvector(p1, f16x2);
+    f16x2 h2 = __builtin_convertvector(p2, f16x2);
+    f16x2 h3 = __builtin_convertvector(p3, f16x2);
+    f16x8 r = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+    return r;
+}
+
+// Value of the same register in lane (l ^ 32): pairs the two k-groups of a 32x32 tile.
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// Byte permute of two dwords (v_perm_b32): selector bytes 0-3 pick from lo, 4-7 from hi.
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel)
+{
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// Pack the low (or high) f16 halves of two dwords: {a.half, b.half}.
+constexpr uint32_t kSelLo = 0x05040100u;
+constexpr uint32_t kSelHi = 0x07060302u;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Order this wave's LDS writes before its later LDS reads (wave-private LDS regions).
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Map a linear block index to a work item so that each XCD (blocks are dealt round-robin
+// over the 8 XCDs) receives one contiguous range of items: items that share a KV head
+// then share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int b, int n_items)
+{
+    const int per = n_items >> 3, rem = n_items & 7;
+    const int x = b & 7, t = b >> 3;
+    return x * per + (x < rem ? x : rem) + t;
+}
+
+}  // namespace nxa

@@ -1,0 +1,95 @@
+"""torch-facing wrappers over the C ABI (device memory and the stream come from torch).
+
+    out = attn_prefill(q, k, v, n_kv_heads=..., q_base_pos=..., n_ctx=...)
+    out = attn_decode(q, k, v, n_kv_heads=..., q_base_pos=..., n_ctx=..., n_splits=64)
+
+Tensors:  q [n_query, n_q_heads, head_dim] f32 or f16;  k, v [n_kv_heads, stride, head_dim]
+f16 (the KV cache layout); out [n_query, n_q_heads, head_dim] f32 or f16.  Everything must
+live on a HIP device: there is no CPU path here, a declined call raises NexusAttnError.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import capi
+
+_DT = {torch.float32: capi.NEXUS_DT_F32, torch.float16: capi.NEXUS_DT_F16}
+
+
+def _kv_view(x: torch.Tensor) -> torch.Tensor:
+    if x.dtype in (torch.int16, torch.uint16):
+        return x
+    if x.dtype != torch.float16:
+        raise TypeError(f"K/V must be float16 (f16 bit patterns), got {x.dtype}")
+    return x
+
+
+def _check_tensors(q, k, v, n_kv_heads):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise RuntimeError(f"{name} must be a device tensor (no CPU path)")
+        if not t.is_contiguous():
+            raise RuntimeError(f"{name} must be contiguous")
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q must be [n_query, Hq, hd], k/v [Hkv, stride, hd]")
+    if q.dtype not in _DT:
+        raise TypeError(f"q dtype {q.dtype} not supported")
+    if k.shape != v.shape or k.shape[0] != n_kv_heads or k.shape[2] != q.shape[2]:
+        raise ValueError(f"k/v shape {tuple(k.shape)} does not match Hkv={n_kv_heads}, hd={q.shape[2]}")
+    _kv_view(k), _kv_view(v)
+
+
+def make_desc_for(q: torch.Tensor, k: torch.Tensor, *, n_kv_heads: int, q_base_pos: int, n_ctx: int,
+                  sliding_window: int = 0, scale: float = 0.0, softcap: float = 0.0,
+                  out_dtype: torch.dtype | None = None) -> capi.AttnDesc:
+    od = out_dtype if out_dtype is not None else q.dtype
+    return capi.make_desc(n_q_heads=q.shape[1], n_kv_heads=n_kv_heads, head_dim=q.shape[2],
+                          n_query=q.shape[0], q_base_pos=q_base_pos, n_ctx=n_ctx,
+                          kv_row_stride=k.shape[1], sliding_window=sliding_window, scale=scale,
+                          softcap=softcap, q_dtype=_DT[q.dtype], o_dtype=_DT[od])
+
+
+def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads: int,
+                 q_base_pos: int, n_ctx: int, sliding_window: int = 0, scale: float = 0.0,
+                 softcap: float = 0.0, out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None,
+                 workspace: torch.Tensor | None = None, split: bool = True) -> torch.Tensor:
+    _check_tensors(q, k, v, n_kv_heads)
+    desc = make_desc_for(q, k, n_kv_heads=n_kv_heads, q_base_pos=q_base_pos, n_ctx=n_ctx,
+                         sliding_window=sliding_window, scale=scale, softcap=softcap,
+                         out_dtype=out_dtype if out is None else out.dtype)
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    ws_ptr, ws_bytes = 0, 0
+    if split:
+        need = capi.prefill_ws_bytes(desc)
+        if need > 0:
+            if workspace is None or workspace.numel() * workspace.element_size() < need:
+                workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    capi.prefill_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws_ptr,
+                     ws_bytes, stream)
+    return out
+
+
+def attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads: int,
+                q_base_pos: int, n_ctx: int, n_splits: int = 0, sliding_window: int = 0,
+                scale: float = 0.0, softcap: float = 0.0, out: torch.Tensor | None = None,
+                out_dtype: torch.dtype | None = None,
+                partial_ws: torch.Tensor | None = None) -> torch.Tensor:
+    _check_tensors(q, k, v, n_kv_heads)
+    desc = make_desc_for(q, k, n_kv_heads=n_kv_heads, q_base_pos=q_base_pos, n_ctx=n_ctx,
+                         sliding_window=sliding_window, scale=scale, softcap=softcap,
+                         out_dtype=out_dtype or (out.dtype if out is not None else torch.float32))
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or torch.float32, device=q.device)
+    need = capi.decode_ws_bytes(desc, n_splits)
+    if need <= 0:
+        raise capi.NexusAttnError(capi.NEXUS_E_UNSUPPORTED, capi.last_error() or "bad shape")
+    if partial_ws is None or partial_ws.numel() * partial_ws.element_size() < need:
+        partial_ws = torch.empty(need // 4, dtype=torch.float32, device=q.device)
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    capi.decode_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                    partial_ws.data_ptr(), n_splits, stream)
+    return out

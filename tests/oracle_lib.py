@@ -1,0 +1,160 @@
+"""Test-side access to the CPU oracle (oracle/libattn_oracle.so) and, when it was built,
+to the reference's own decode code (oracle/_ref/libnexus_ref_attn.so).
+
+Only tests, __graft_entry__.smoke() and bench.py's CPU-baseline leg use this module.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_SO = ROOT / "oracle" / "libattn_oracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libnexus_ref_attn.so"
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i, _l, _f, _d = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double
+
+_oracle = None
+_ref = None
+
+
+def oracle() -> ctypes.CDLL:
+    global _oracle
+    if _oracle is None:
+        if not ORACLE_SO.exists():
+            raise RuntimeError(f"{ORACLE_SO} missing: run `make -C oracle` (or __graft_entry__.build())")
+        lib = ctypes.CDLL(str(ORACLE_SO))
+        lib.nx_f16_bits_to_f32.argtypes = [ctypes.c_uint16]
+        lib.nx_f16_bits_to_f32.restype = _f
+        lib.nx_f32_to_f16_trunc.argtypes = [_f]
+        lib.nx_f32_to_f16_trunc.restype = ctypes.c_uint16
+        lib.nx_f32_to_f16_rne.argtypes = [_f]
+        lib.nx_f32_to_f16_rne.restype = ctypes.c_uint16
+        lib.nx_f32_to_f16_trunc_n.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        lib.nx_f32_to_f16_rne_n.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        lib.nx_f16_to_f32_n.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+        lib.oracle_attn_batch.argtypes = [_f32p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _l, _i, _i, _i, _f, _f, _i]
+        lib.oracle_attn_batch_rows.argtypes = [_f32p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _l, _i, _i, _i,
+                                               _f, _f, _i32p, _i, _i]
+        lib.oracle_cached_scores.argtypes = [_f32p, _f32p, _u16p, _u16p, _l, _i, _i, _i, _i, _f, _f, _i]
+        lib.oracle_split_partials.argtypes = [_f32p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _l, _i, _i, _f, _i, _i]
+        lib.oracle_split_combine.argtypes = [_f32p, _f32p, _i, _i, _i]
+        lib.oracle_naive_f64.argtypes = [_f32p, _u16p, _u16p, _f64p, _i, _i, _i, _i, _l, _i, _i, _i, _d, _d]
+        _oracle = lib
+    return _oracle
+
+
+def ref_available() -> bool:
+    return REF_SO.exists()
+
+
+def ref() -> ctypes.CDLL:
+    global _ref
+    if _ref is None:
+        if not REF_SO.exists():
+            raise RuntimeError(f"{REF_SO} missing: it is built from /root/reference by `make -C oracle ref`")
+        lib = ctypes.CDLL(str(REF_SO))
+        lib.ref_forward_cached_scores.argtypes = [_f32p, _f32p, _u16p, _u16p, _l, _i, _i, _i, _i, _f, _f, _i]
+        lib.ref_forward_cached_scores.restype = _i
+        lib.ref_kv_store_pack.argtypes = [_f32p, _f32p, _i, _i, _i, _u16p, _u16p]
+        lib.ref_kv_store_pack.restype = _i
+        lib.ref_kv_capacity_after.argtypes = [_i, _i]
+        lib.ref_kv_capacity_after.restype = _l
+        lib.ref_f32_to_f16_rne.argtypes = [_f]
+        lib.ref_f32_to_f16_rne.restype = ctypes.c_uint16
+        lib.ref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        lib.ref_f16_to_f32.restype = _f
+        _ref = lib
+    return _ref
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def attn_batch(q, k, v, *, n_kv_heads, n_ctx, q_base_pos, sliding_window=0, scale=0.0,
+               softcap=0.0, n_threads=1):
+    """Transformer::attn_batch_cpu restated.  q [nq, Hq, hd] f32; k, v [Hkv, stride, hd] u16."""
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    nq, hq, hd = q.shape
+    sc = scale if scale > 0 else 1.0 / np.sqrt(hd)
+    out = np.zeros_like(q)
+    oracle().oracle_attn_batch(q, k, v, out, hq, n_kv_heads, hd, n_ctx, k.shape[1], nq, q_base_pos,
+                               sliding_window, sc, softcap, n_threads)
+    return out
+
+
+def attn_batch_rows(q, k, v, rows, *, n_kv_heads, n_ctx, q_base_pos, scale=0.0, n_threads=1):
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    nq, hq, hd = q.shape
+    sc = scale if scale > 0 else 1.0 / np.sqrt(hd)
+    out = np.zeros_like(q)
+    rows = _c(rows, np.int32)
+    oracle().oracle_attn_batch_rows(q, k, v, out, hq, n_kv_heads, hd, n_ctx, k.shape[1], nq, q_base_pos,
+                                    0, sc, 0.0, rows, len(rows), n_threads)
+    return out
+
+
+def cached_scores(q, k, v, *, n_kv_heads, pos, scale=0.0, softcap=0.0, n_threads=1):
+    """AttentionLayer::forward_cached_scores restated.  q [Hq, hd]."""
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    hq, hd = q.shape
+    out = np.zeros_like(q)
+    oracle().oracle_cached_scores(q, out, k, v, k.shape[1], hq, n_kv_heads, hd, pos, scale, softcap, n_threads)
+    return out
+
+
+def ref_cached_scores(q, k, v, *, n_kv_heads, pos, scale=0.0, softcap=0.0, n_threads=1):
+    """The reference's own forward_cached_scores (compiled from its sources)."""
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    hq, hd = q.shape
+    out = np.zeros_like(q)
+    rc = ref().ref_forward_cached_scores(q, out, k, v, k.shape[1], hq, n_kv_heads, hd, pos, scale,
+                                         softcap, n_threads)
+    assert rc == 0
+    return out
+
+
+def split_partials(q, k, v, *, n_kv_heads, n_ctx, q_base_pos, n_chunks, chunk, scale=0.0):
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    nq, hq, hd = q.shape
+    sc = scale if scale > 0 else 1.0 / np.sqrt(hd)
+    part = np.zeros((nq * hq, n_chunks, hd + 2), np.float32)
+    oracle().oracle_split_partials(q, k, v, part, hq, n_kv_heads, hd, n_ctx, k.shape[1], nq, q_base_pos,
+                                   sc, n_chunks, chunk)
+    return part
+
+
+def split_combine(part):
+    part = _c(part, np.float32)
+    rows, n_chunks, hd2 = part.shape
+    out = np.zeros((rows, hd2 - 2), np.float32)
+    oracle().oracle_split_combine(part, out, rows, hd2 - 2, n_chunks)
+    return out
+
+
+def naive_f64(q, k, v, *, n_kv_heads, n_ctx, q_base_pos, sliding_window=0, scale=0.0, softcap=0.0):
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    nq, hq, hd = q.shape
+    sc = scale if scale > 0 else 1.0 / np.sqrt(hd)
+    out = np.zeros(q.shape, np.float64)
+    oracle().oracle_naive_f64(q, k, v, out, hq, n_kv_heads, hd, n_ctx, k.shape[1], nq, q_base_pos,
+                              sliding_window, sc, softcap)
+    return out
+
+
+def max_abs(a, b) -> float:
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)))) if np.size(a) else 0.0
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    den = np.sqrt(np.sum(b * b))
+    return float(np.sqrt(np.sum((a - b) ** 2)) / max(den, 1e-30))

@@ -1,0 +1,120 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol the header
+declares, and declines unsupported or invalid calls before touching any output (the
+reference's `return false` before side effects, vulkan_backend.h:4267-4277)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from nexus_amd import capi
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "nexus_hip_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(nexus_hip_attn_[a-z_0-9]+)\s*\(", text, re.M)))
+
+
+def test_header_declares_what_the_binding_knows():
+    assert declared_functions() == sorted(capi.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert "gfx950" in capi.version()
+
+
+def test_desc_layout_matches_header(tmp_path):
+    """The ctypes mirror of nexus_attn_desc has the C compiler's size and offsets."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler on this host")
+    fields = [f[0] for f in capi.AttnDesc._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "nexus_hip_attn.h"\nint main(void){'
+                   'printf("%zu", sizeof(nexus_attn_desc));'
+                   + "".join(f'printf(" %zu", offsetof(nexus_attn_desc, {f}));' for f in fields)
+                   + "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(capi.AttnDesc)
+    assert got[1:] == [getattr(capi.AttnDesc, f).offset for f in fields]
+
+
+def _desc(**kw):
+    base = dict(n_q_heads=8, n_kv_heads=2, head_dim=128, n_query=16, q_base_pos=32, n_ctx=48)
+    base.update(kw)
+    return capi.make_desc(**base)
+
+
+BAD = [
+    (dict(head_dim=96), capi.NEXUS_E_UNSUPPORTED),
+    (dict(head_dim=320), capi.NEXUS_E_UNSUPPORTED),
+    (dict(n_q_heads=7, n_kv_heads=2), capi.NEXUS_E_UNSUPPORTED),
+    (dict(n_kv_heads=0), capi.NEXUS_E_UNSUPPORTED),
+    (dict(n_query=0), capi.NEXUS_E_INVALID),
+    (dict(n_ctx=0), capi.NEXUS_E_INVALID),
+    (dict(q_base_pos=-1), capi.NEXUS_E_INVALID),
+    (dict(kv_row_stride=47), capi.NEXUS_E_INVALID),
+    (dict(sliding_window=-3), capi.NEXUS_E_INVALID),
+    (dict(scale=float("nan")), capi.NEXUS_E_INVALID),
+    (dict(softcap=-1.0), capi.NEXUS_E_INVALID),
+    (dict(q_dtype=7), capi.NEXUS_E_UNSUPPORTED),
+]
+
+
+@pytest.mark.parametrize("kw,code", BAD)
+def test_declines_before_side_effects(kw, code):
+    d = _desc(**kw)
+    out = np.full(64, 7.0, np.float32)
+    dummy = np.zeros(64, np.float32)
+    p = dummy.ctypes.data
+    rc = capi.prefill_raw(d, p, p, p, out.ctypes.data, 0, 0, 0, check=False)
+    assert rc == code, capi.last_error()
+    assert capi.last_error()
+    rc = capi.decode_raw(d, p, p, p, out.ctypes.data, p, 4, 0, check=False)
+    assert rc == code
+    assert np.all(out == 7.0)
+
+
+def test_null_pointers_declined():
+    d = _desc()
+    out = np.full(8, 3.0, np.float32)
+    rc = capi.prefill_raw(d, 0, 0, 0, out.ctypes.data, 0, 0, 0, check=False)
+    assert rc == capi.NEXUS_E_INVALID
+    x = np.zeros(4, np.float32).ctypes.data
+    rc = capi.decode_raw(d, x, x, x, out.ctypes.data, 0, 4, 0, check=False)
+    assert rc == capi.NEXUS_E_WORKSPACE
+    rc = capi.decode_raw(d, x, x, x, out.ctypes.data, x, 5000, 0, check=False)
+    assert rc == capi.NEXUS_E_UNSUPPORTED
+    assert np.all(out == 3.0)
+
+
+def test_workspace_sizes():
+    # decode: [n_query*Hq][n_splits][hd+2] f32
+    d = capi.make_desc(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=1, q_base_pos=61439, n_ctx=61440)
+    assert capi.decode_ws_bytes(d, 64) == 40 * 64 * 130 * 4
+    assert capi.decode_ws_bytes(d, 0) == 40 * capi.decode_default_splits(d) * 130 * 4
+    assert capi.decode_ws_bytes(_desc(head_dim=96), 4) == 0
+    # a cold 8192 prompt with 40 heads fills the GPU unsplit: no workspace
+    cold = capi.make_desc(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=8192, q_base_pos=0, n_ctx=8192)
+    assert capi.prefill_ws_bytes(cold) == 0
+    # 4 speculative drafts x G=8 rows run through the split-KV path
+    mtp = capi.make_desc(n_q_heads=16, n_kv_heads=2, head_dim=256, n_query=4, q_base_pos=32768, n_ctx=32772)
+    assert capi.prefill_ws_bytes(mtp) == capi.decode_ws_bytes(mtp, 0) > 0
+
+
+def test_algorithmic_work_formulas():
+    # cfg2 / cfg3 pair counts from the survey: 2,228,480 and 33,558,528 pairs per head
+    assert capi.prefill_flops(40, 128, 512, 4096, 4608) == 4 * 128 * 40 * 2_228_480
+    assert capi.prefill_flops(40, 128, 8192, 0, 8192) == 4 * 128 * 40 * 33_558_528
+    assert capi.decode_bytes(8, 128, 61440, 40, 1) == 2 * 8 * 61440 * 128 * 2 + 40 * 128 * 8

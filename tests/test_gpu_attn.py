@@ -1,0 +1,236 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Tolerance: max-abs 2e-3 and rel-L2 1e-3 of the fp32-accumulated
+output against the reference's CPU attention on the same seeded inputs; f16 outputs are
+upcast before comparing.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from nexus_amd import capi, ops
+from nexus_amd.inputs import make_case
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-3
+REL_L2 = 1e-3
+
+
+def dev(x):
+    if x.dtype == np.uint16:
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).cuda()
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def assert_close(got, ref, what=""):
+    ma, rl = O.max_abs(got, ref), O.rel_l2(got, ref)
+    print(f"[parity] {what} max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    assert ma < MAX_ABS and rl < REL_L2, f"{what}: max_abs={ma:.3e} rel_l2={rl:.3e}"
+
+
+def run_prefill(q, k, v, *, hkv, n_ctx, q_base, q_f16=False, o_f16=False, sw=0, cap=0.0, split=True):
+    qt = dev(q)
+    if q_f16:
+        qt = qt.half()
+    out = ops.attn_prefill(qt, dev(k), dev(v), n_kv_heads=hkv, q_base_pos=q_base, n_ctx=n_ctx,
+                           sliding_window=sw, softcap=cap, out_dtype=torch.float16 if o_f16 else torch.float32,
+                           split=split)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def run_decode(q, k, v, *, hkv, n_ctx, q_base, n_splits=0, sw=0, cap=0.0, ws=None):
+    out = ops.attn_decode(dev(q), dev(k), dev(v), n_kv_heads=hkv, q_base_pos=q_base, n_ctx=n_ctx,
+                          n_splits=n_splits, sliding_window=sw, softcap=cap, partial_ws=ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# ------------------------------------------------------------------------ prefill
+
+PREFILL_CASES = [
+    # (Hq, Hkv, hd, n_query, q_base, extra_stride, q_f16, o_f16, sw, cap)
+    (8, 2, 128, 128, 0, 0, True, True, 0, 0.0),        # one full block, cold
+    (8, 2, 128, 200, 0, 0, True, True, 0, 0.0),        # ragged second block
+    (10, 2, 128, 77, 300, 5, True, False, 0, 0.0),     # chunk after cache, padded stride
+    (4, 4, 64, 150, 17, 0, False, False, 0, 0.0),      # MHA, hd 64, f32 q/o
+    (16, 2, 256, 96, 40, 3, True, True, 0, 0.0),       # hd 256, G=8
+    (6, 2, 192, 70, 10, 0, True, True, 0, 0.0),        # hd 192
+    (8, 8, 128, 130, 0, 0, True, True, 50, 0.0),       # sliding window
+    (8, 4, 128, 100, 60, 0, False, False, 0, 30.0),    # softcap
+    (8, 2, 128, 64, 2000, 0, True, True, 0, 0.0),      # long cache, short chunk (split path)
+    (40, 8, 128, 33, 1000, 0, True, True, 0, 0.0),     # cfg-2 head layout, small
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,extra,qf16,of16,sw,cap", PREFILL_CASES)
+def test_prefill_vs_oracle(hip, hq, hkv, hd, nq, base, extra, qf16, of16, sw, cap):
+    n_ctx = base + nq
+    print(f"[case] prefill hq={hq} hkv={hkv} hd={hd} nq={nq} base={base} sw={sw} cap={cap}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx,
+                        kv_stride=n_ctx + extra, seed=nq + base, q_f16=qf16)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, q_f16=qf16, o_f16=of16, sw=sw, cap=cap)
+    ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, sliding_window=sw,
+                       softcap=cap, n_threads=8)
+    assert_close(got, ref, f"prefill {hq}/{hkv} hd{hd} nq{nq}@{base}")
+
+
+def test_prefill_queries_past_cache_and_short_cache(hip):
+    """n_ctx < q_base + n_query: late queries see [0, n_ctx-1] (transformer.h:8670)."""
+    hq, hkv, hd, nq, base, n_ctx = 8, 2, 128, 150, 40, 100
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=3, q_f16=True)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, q_f16=True)
+    ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8)
+    assert_close(got, ref, "past-cache")
+
+
+def test_prefill_golden(hip, golden):
+    hq, hkv, hd, q_base, nq, n_ctx = (int(x) for x in golden["pre_a_meta"])
+    got = run_prefill(golden["pre_a_q"], golden["pre_a_k"], golden["pre_a_v"], hkv=hkv, n_ctx=n_ctx, q_base=q_base)
+    assert_close(got, golden["pre_a_out"], "golden pre_a")
+
+
+def test_prefill_split_equals_unsplit(hip):
+    hq, hkv, hd, nq, base = 8, 2, 128, 256, 3000
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=4, q_f16=True)
+    a = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, split=True)
+    b = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, split=False)
+    assert O.max_abs(a, b) < 1e-3 and O.rel_l2(a, b) < 5e-4
+
+
+def test_prefill_chunked_equals_cold_rows(hip):
+    """Rows of a chunk appended after a cache == the same rows of a cold prefill."""
+    hq, hkv, hd, base, nq = 8, 2, 128, 384, 256
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=base + nq, n_ctx=base + nq, seed=5, q_f16=True)
+    cold = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=0, q_f16=True, split=False)
+    chunk = run_prefill(q[base:], k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, split=False)
+    assert O.max_abs(chunk, cold[base:]) < 1e-3
+
+
+# ------------------------------------------------------------------------ decode
+
+DECODE_CASES = [
+    # (Hq, Hkv, hd, n_query, q_base, n_ctx, n_splits, extra_stride)
+    (16, 4, 128, 1, 4095, 4096, 0, 0),          # cfg 1
+    (16, 4, 128, 1, 4095, 4096, 1, 0),
+    (40, 8, 128, 1, 3000, 3001, 64, 7),         # cfg 4 layout, short
+    (40, 8, 128, 1, 777, 778, 13, 0),           # ragged splits
+    (16, 2, 256, 4, 2000, 2004, 0, 0),          # MTP verify layout (cfg 5), short
+    (16, 2, 256, 4, 2000, 2004, 5, 0),
+    (8, 8, 64, 1, 0, 1, 0, 0),                  # single key
+    (12, 2, 192, 3, 100, 103, 0, 0),            # G=6 x 3 drafts, hd 192
+    (64, 1, 128, 1, 500, 501, 0, 0),            # G=64: two row groups
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,n_ctx,splits,extra", DECODE_CASES)
+def test_decode_vs_oracle(hip, hq, hkv, hd, nq, base, n_ctx, splits, extra):
+    print(f"[case] decode hq={hq} hkv={hkv} hd={hd} nq={nq} base={base} ctx={n_ctx} splits={splits}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx,
+                        kv_stride=n_ctx + extra, seed=n_ctx + hq)
+    got = run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits)
+    ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8)
+    assert_close(got, ref, f"decode {hq}/{hkv} hd{hd} nq{nq}@{base}")
+    if nq == 1:
+        dec = O.cached_scores(q[0], k, v, n_kv_heads=hkv, pos=base, n_threads=8)
+        assert_close(got[0], dec, "decode vs forward_cached_scores restatement")
+
+
+@pytest.mark.parametrize("name", ["dec_a", "dec_b", "dec_d"])
+def test_decode_golden(hip, golden, name):
+    hq, hkv, hd, pos = (int(x) for x in golden[f"{name}_meta"])
+    q = golden[f"{name}_q"][None]
+    got = run_decode(q, golden[f"{name}_k"], golden[f"{name}_v"], hkv=hkv, n_ctx=pos + 1, q_base=pos)
+    assert_close(got[0], golden[f"{name}_out"], f"golden {name}")
+
+
+def test_decode_sliding_window_and_softcap(hip):
+    hq, hkv, hd, nq, base = 8, 2, 128, 2, 900
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=6)
+    for sw, cap in ((100, 0.0), (0, 20.0), (33, 10.0)):
+        got = run_decode(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, sw=sw, cap=cap)
+        ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base, sliding_window=sw,
+                           softcap=cap, n_threads=8)
+        assert_close(got, ref, f"decode sw={sw} cap={cap}")
+
+
+def test_decode_partials_have_reference_meaning(hip):
+    """partial_ws[row][split] = (sum e^{s-m} v, m, l) over the split's keys, as
+    qwen35_attn_part.comp:3 defines them (m is the split's max score)."""
+    hq, hkv, hd, base = 8, 2, 128, 1023
+    n_ctx = base + 1
+    splits = 8
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=n_ctx, seed=7)
+    ws = torch.zeros(hq * splits * (hd + 2), dtype=torch.float32, device="cuda")
+    run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits, ws=ws)
+    got = ws.cpu().numpy().reshape(hq, splits, hd + 2)
+    chunk = ((n_ctx + splits - 1) // splits + 31) // 32 * 32
+    ref = O.split_partials(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_chunks=splits, chunk=chunk)
+    assert np.max(np.abs(got[:, :, hd] - ref[:, :, hd])) < 1e-4                     # m
+    assert O.rel_l2(got[:, :, hd + 1], ref[:, :, hd + 1]) < 1e-3                    # l
+    assert O.rel_l2(got[:, :, :hd], ref[:, :, :hd]) < 1e-3                          # acc
+
+
+def test_decode_split_count_invariance(hip):
+    hq, hkv, hd, base = 16, 4, 128, 5000
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=base + 1, seed=8)
+    outs = [run_decode(q, k, v, hkv=hkv, n_ctx=base + 1, q_base=base, n_splits=s) for s in (1, 3, 64, 157)]
+    for o in outs[1:]:
+        assert O.max_abs(o, outs[0]) < 1e-5
+
+
+# ------------------------------------------------------------------ declines (device)
+
+def test_declined_call_leaves_device_output_untouched(hip):
+    q = torch.randn(4, 8, 96, device="cuda")
+    k = torch.zeros(2, 16, 96, dtype=torch.float16, device="cuda")
+    out = torch.full((4, 8, 96), 5.0, device="cuda")
+    d = capi.make_desc(n_q_heads=8, n_kv_heads=2, head_dim=96, n_query=4, q_base_pos=12, n_ctx=16)
+    rc = capi.prefill_raw(d, q.data_ptr(), k.data_ptr(), k.data_ptr(), out.data_ptr(), 0, 0,
+                          torch.cuda.current_stream().cuda_stream, check=False)
+    assert rc == capi.NEXUS_E_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert torch.all(out == 5.0)
+
+
+# ------------------------------------------------------------------ full-size configs
+
+def _sample_rows(nq, hq, n, seed):
+    rng = np.random.default_rng(seed)
+    rows = rng.choice(nq * hq, size=min(n, nq * hq), replace=False)
+    # always include the first and last query rows (shortest and longest windows)
+    return np.unique(np.concatenate([rows, [0, hq - 1, nq * hq - 1, (nq - 1) * hq]])).astype(np.int32)
+
+
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg3"])
+def test_prefill_full_config_sampled_rows(hip, cfg):
+    hq, hkv, hd = 40, 8, 128
+    nq, base = (512, 4096) if cfg == "cfg2" else (8192, 0)
+    n_ctx = base + nq
+    print(f"[case] {cfg} full size", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=2024, q_f16=True)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, q_f16=True, o_f16=True)
+    assert np.all(np.isfinite(got))
+    rows = _sample_rows(nq, hq, 256, 1)
+    ref = O.attn_batch_rows(q, k, v, rows, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8)
+    g = got.reshape(nq * hq, hd)[rows]
+    r = ref.reshape(nq * hq, hd)[rows]
+    assert_close(g, r, f"{cfg} sampled rows")
+
+
+def test_decode_full_cfg4(hip):
+    hq, hkv, hd, n_ctx = 40, 8, 128, 61440
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=n_ctx, seed=4)
+    got = run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=n_ctx - 1, n_splits=64)
+    ref = O.cached_scores(q[0], k, v, n_kv_heads=hkv, pos=n_ctx - 1, n_threads=8)
+    assert_close(got[0], ref, "cfg4 full")
+
+
+def test_verify_full_cfg5(hip):
+    hq, hkv, hd, base, nq = 16, 2, 256, 32768, 4
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=5)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base)      # routed to split-KV
+    ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base, n_threads=8)
+    assert_close(got, ref, "cfg5 full")

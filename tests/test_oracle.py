@@ -1,0 +1,308 @@
+"""Pins for the CPU oracle (oracle/attn_oracle.c) -- CPU only.
+
+Each oracle function is checked against something it does not restate: the reference's
+own compiled code (oracle/_ref, when present), committed fixtures that code wrote
+(tests/golden/golden_attn.npz), library routines (numpy float16), float64 brute force,
+and closed forms chosen so that a dropped term, a wrong sign, an off-by-one in the
+causal window or a transposed operand fails at least one of them.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from nexus_amd.inputs import f32_to_f16_trunc, f16_to_f32, make_case, normal
+
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+
+
+# ---------------------------------------------------------------- f16 conversions
+
+def test_f16_decode_exhaustive_vs_numpy():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = np.zeros(65536, np.float32)
+    O.oracle().nx_f16_to_f32_n(bits, got, 65536)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@needs_ref
+def test_f16_decode_exhaustive_vs_reference():
+    r = O.ref()
+    bits = np.arange(65536, dtype=np.uint16)
+    got = np.zeros(65536, np.float32)
+    O.oracle().nx_f16_to_f32_n(bits, got, 65536)
+    want = np.array([r.ref_f16_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _rand_f32(n, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    return x[~np.isnan(x)]
+
+
+def test_f16_rne_vs_numpy_2m_patterns():
+    x = _rand_f32(2_000_000, 1)
+    got = np.zeros(x.size, np.uint16)
+    O.oracle().nx_f32_to_f16_rne_n(x, got, x.size)
+    assert np.array_equal(got, x.astype(np.float16).view(np.uint16))
+    y = (normal(3, 200_000) * np.float32(1e-5)).astype(np.float32)     # dense in the subnormal range
+    got = np.zeros(y.size, np.uint16)
+    O.oracle().nx_f32_to_f16_rne_n(y, got, y.size)
+    assert np.array_equal(got, y.astype(np.float16).view(np.uint16))
+
+
+@needs_ref
+def test_f16_rne_vs_reference():
+    x = _rand_f32(100_000, 2)
+    got = np.zeros(x.size, np.uint16)
+    O.oracle().nx_f32_to_f16_rne_n(x, got, x.size)
+    r = O.ref()
+    want = np.array([r.ref_f32_to_f16_rne(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f16_trunc_is_nearest_toward_zero():
+    """Truncating store = the f16 neighbour of x toward zero, in the normal range."""
+    x = _rand_f32(400_000, 4)
+    ax = np.abs(x)
+    x = x[(ax >= 2.0**-14) & (ax < 65504.0)]
+    got = np.zeros(x.size, np.uint16)
+    O.oracle().nx_f32_to_f16_trunc_n(x, got, x.size)
+    h = got.view(np.float16)
+    hv = h.astype(np.float64)
+    assert np.all(np.abs(hv) <= np.abs(x.astype(np.float64)))
+    nxt = np.nextafter(h, np.copysign(np.float16(np.inf), h)).astype(np.float64)
+    assert np.all(np.abs(nxt) > np.abs(x.astype(np.float64)))
+    assert np.array_equal(np.signbit(hv), np.signbit(x))
+
+
+def test_f16_trunc_special_cases():
+    f = O.oracle().nx_f32_to_f16_trunc
+    assert f(0.0) == 0x0000 and f(-0.0) == 0x8000
+    assert f(6.0e-5) == 0x0000            # below 2^-14: flushed (no subnormals)
+    assert f(-3.0e-5) == 0x8000
+    assert f(2.0**-14) == 0x0400
+    assert f(65504.0) == 0x7BFF and f(65519.0) == 0x7BFF
+    assert f(65536.0) == 0x7C00 and f(-1e9) == 0xFC00
+    assert f(float("inf")) == 0x7C00 and f(float("nan")) == 0x7C00
+    assert f(1.0 + 2.0**-10 + 2.0**-11) == 0x3C01     # truncation, not rounding
+
+
+def test_f16_trunc_matches_numpy_restatement():
+    x = _rand_f32(300_000, 5)
+    got = np.zeros(x.size, np.uint16)
+    O.oracle().nx_f32_to_f16_trunc_n(x, got, x.size)
+    assert np.array_equal(got, f32_to_f16_trunc(x))
+
+
+def test_kv_store_golden(golden):
+    """KVCache::store + pack_k/pack_v bits written by the reference's own KVCache."""
+    hkv, hd, ntok = golden["kv_meta"]
+    kf, vf = golden["kv_kf"], golden["kv_vf"]
+    for src, packed in ((kf, golden["kv_kpacked"]), (vf, golden["kv_vpacked"])):
+        bits = np.zeros(src.size, np.uint16)
+        O.oracle().nx_f32_to_f16_trunc_n(np.ascontiguousarray(src.ravel()), bits, src.size)
+        mine = bits.reshape(ntok, hkv, hd).transpose(1, 0, 2)     # [tok][h][d] -> packed [h][tok][d]
+        assert np.array_equal(mine, packed)
+        assert np.array_equal(f32_to_f16_trunc(src).reshape(ntok, hkv, hd).transpose(1, 0, 2), packed)
+
+
+# ------------------------------------------------------- decode: forward_cached_scores
+
+@pytest.mark.parametrize("name", ["dec_a", "dec_b", "dec_c", "dec_d"])
+def test_cached_scores_vs_golden(golden, name):
+    hq, hkv, hd, pos = (int(x) for x in golden[f"{name}_meta"])
+    scale, cap = (float(x) for x in golden[f"{name}_fmeta"])
+    y = O.cached_scores(golden[f"{name}_q"], golden[f"{name}_k"], golden[f"{name}_v"],
+                        n_kv_heads=hkv, pos=pos, scale=scale, softcap=cap)
+    ref = golden[f"{name}_out"]
+    assert O.max_abs(y, ref) < 2e-6 and O.rel_l2(y, ref) < 1e-5
+
+
+@needs_ref
+@pytest.mark.parametrize("hq,hkv,hd,pos,cap", [(16, 4, 128, 1500, 0.0), (40, 8, 128, 700, 0.0),
+                                               (6, 3, 64, 2, 0.0), (8, 1, 256, 333, 50.0)])
+def test_cached_scores_vs_reference(hq, hkv, hd, pos, cap):
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=pos + 1,
+                        kv_stride=pos + 17, seed=pos)
+    y = O.cached_scores(q[0], k, v, n_kv_heads=hkv, pos=pos, softcap=cap, n_threads=4)
+    r = O.ref_cached_scores(q[0], k, v, n_kv_heads=hkv, pos=pos, softcap=cap, n_threads=4)
+    assert O.max_abs(y, r) < 2e-6 and O.rel_l2(y, r) < 1e-5
+
+
+# ------------------------------------------------------------ prefill: attn_batch_cpu
+
+def test_attn_batch_vs_golden_prefill(golden):
+    """Each chunked-prefill row equals the reference's decode at that query's position."""
+    hq, hkv, hd, q_base, nq, n_ctx = (int(x) for x in golden["pre_a_meta"])
+    y = O.attn_batch(golden["pre_a_q"], golden["pre_a_k"], golden["pre_a_v"], n_kv_heads=hkv,
+                     n_ctx=n_ctx, q_base_pos=q_base)
+    ref = golden["pre_a_out"]
+    assert O.max_abs(y, ref) < 2e-6 and O.rel_l2(y, ref) < 1e-5
+
+
+@needs_ref
+@pytest.mark.parametrize("hq,hkv,hd,q_base,nq,extra", [(8, 2, 128, 200, 33, 0), (5, 1, 64, 0, 40, 7),
+                                                        (12, 4, 256, 31, 9, 3)])
+def test_attn_batch_rows_vs_reference_decode(hq, hkv, hd, q_base, nq, extra):
+    """attn_batch row i == forward_cached_scores at q_base + i; keys past the query
+    (n_ctx > q_base + nq would not change it) and the stride padding are ignored."""
+    n_ctx = q_base + nq
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx,
+                        kv_stride=n_ctx + extra, seed=hq * 7 + nq)
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=q_base)
+    for i in range(nq):
+        r = O.ref_cached_scores(q[i], k, v, n_kv_heads=hkv, pos=q_base + i)
+        assert O.max_abs(y[i], r) < 2e-6 and O.rel_l2(y[i], r) < 1e-5, i
+
+
+# the reference's own batched-attention test shapes (test_attn_batch.cpp:183-204), N scaled down
+REF_TEST_CASES = [
+    ("qwen_full_hd256", 24, 4, 256, 96, 0, 0, 0.0),
+    ("mha_hd128", 32, 32, 128, 64, 0, 0, 0.0),
+    ("gqa_hd128", 32, 8, 128, 64, 0, 0, 0.0),
+    ("gqa_hd64", 16, 4, 64, 100, 0, 0, 0.0),
+    ("continuation", 24, 4, 256, 32, 600, 0, 0.0),
+    ("swa_window256", 32, 8, 128, 300, 0, 256, 0.0),
+    ("softcap30_hd128", 16, 16, 128, 80, 0, 0, 30.0),
+    ("N1_hd256", 24, 4, 256, 1, 0, 0, 0.0),
+]
+
+
+@pytest.mark.parametrize("name,hq,hkv,hd,nq,base,sw,cap", REF_TEST_CASES)
+def test_attn_batch_vs_f64_bruteforce(name, hq, hkv, hd, nq, base, sw, cap):
+    n_ctx = base + nq
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=len(name))
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, sliding_window=sw,
+                     softcap=cap, n_threads=8)
+    r = O.naive_f64(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, sliding_window=sw, softcap=cap)
+    assert O.max_abs(y, r) < 2e-4          # test_attn_batch.cpp:169
+
+
+def test_closed_form_single_key():
+    q, k, v = make_case(n_q_heads=4, n_kv_heads=2, head_dim=64, n_query=3, n_ctx=1, seed=3)
+    y = O.attn_batch(q, k, v, n_kv_heads=2, n_ctx=1, q_base_pos=0)
+    vv = f16_to_f32(v[:, 0])                           # [Hkv][hd]
+    for h in range(4):
+        for i in range(3):
+            assert np.array_equal(y[i, h], vv[h * 2 // 4])
+
+
+def test_closed_form_zero_query_is_mean_of_visible_values():
+    hq, hkv, hd, base, nq = 6, 3, 64, 10, 5
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=4)
+    q[:] = 0.0
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base)
+    vf = f16_to_f32(v)
+    for i in range(nq):
+        for h in range(hq):
+            want = vf[h * hkv // hq, : base + i + 1].mean(axis=0)
+            assert np.max(np.abs(y[i, h] - want)) < 1e-5
+
+
+def test_closed_form_one_hot_key_selects_its_value():
+    """K_j = c*q for one key j (large c), others orthogonal-ish: out ~= V_j."""
+    hd = 64
+    q = np.zeros((1, 1, hd), np.float32)
+    q[0, 0, 3] = 1.0
+    n_ctx = 9
+    kf = np.zeros((1, n_ctx, hd), np.float32)
+    kf[0, 5, 3] = 200.0
+    k = kf.astype(np.float16).view(np.uint16)
+    v = normal(9, n_ctx * hd).reshape(1, n_ctx, hd).astype(np.float16).view(np.uint16)
+    y = O.attn_batch(q, k, v, n_kv_heads=1, n_ctx=n_ctx, q_base_pos=n_ctx - 1)
+    assert np.max(np.abs(y[0, 0] - f16_to_f32(v[0, 5]))) < 1e-6
+    # the same key beyond the query's position is masked: query at position 4 cannot see key 5
+    y2 = O.attn_batch(q, k, v, n_kv_heads=1, n_ctx=n_ctx, q_base_pos=4)
+    assert np.max(np.abs(y2[0, 0] - f16_to_f32(v[0, :5]).mean(axis=0))) < 1e-5
+
+
+def test_window_of_one_returns_own_value():
+    hq, hkv, hd, base, nq = 4, 2, 64, 20, 6
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=5)
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base, sliding_window=1)
+    vf = f16_to_f32(v)
+    for i in range(nq):
+        for h in range(hq):
+            assert np.array_equal(y[i, h], vf[h * hkv // hq, base + i])
+
+
+def test_softcap_limits():
+    hq, hkv, hd, nq = 4, 2, 64, 12
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=nq, seed=6)
+    plain = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=nq, q_base_pos=0)
+    huge = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=nq, q_base_pos=0, softcap=1e6)
+    assert O.max_abs(plain, huge) < 1e-6
+    tiny = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=nq, q_base_pos=0, softcap=1e-6)
+    vf = f16_to_f32(v)
+    for i in range(nq):
+        for h in range(hq):
+            assert np.max(np.abs(tiny[i, h] - vf[h * hkv // hq, : i + 1].mean(axis=0))) < 1e-4
+
+
+def test_queries_past_the_cache_see_all_keys():
+    """q_base + i >= n_ctx: the window ends at n_ctx - 1 (transformer.h:8670)."""
+    hq, hkv, hd = 4, 1, 64
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=3, n_ctx=10, seed=8)
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=10, q_base_pos=20)
+    r = O.naive_f64(q, k, v, n_kv_heads=hkv, n_ctx=10, q_base_pos=20)
+    assert O.max_abs(y, r) < 1e-6
+    y0 = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=10, q_base_pos=9)
+    assert O.max_abs(y, y0) < 1e-7
+
+
+def test_chunked_rows_equal_cold_prefill_rows():
+    hq, hkv, hd, base, nq = 8, 2, 128, 48, 16
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=base + nq, n_ctx=base + nq, seed=9)
+    cold = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=0)
+    chunk = O.attn_batch(q[base:], k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base)
+    assert np.array_equal(chunk, cold[base:])
+
+
+def test_gqa_head_permutation_equivariance():
+    hq, hkv, hd, nq = 6, 2, 64, 10
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=nq, seed=10)
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=nq, q_base_pos=0)
+    perm_kv = [1, 0]
+    perm_q = [3, 4, 5, 0, 1, 2]
+    y2 = O.attn_batch(q[:, perm_q], k[perm_kv], v[perm_kv], n_kv_heads=hkv, n_ctx=nq, q_base_pos=0)
+    assert np.array_equal(y2, y[:, perm_q])
+
+
+def test_causality_future_keys_do_not_matter():
+    hq, hkv, hd, nq = 4, 2, 64, 8
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=nq + 5, seed=12)
+    y = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=nq + 5, q_base_pos=0)
+    k2, v2 = k.copy(), v.copy()
+    k2[:, nq:] ^= 0x1234
+    v2[:, nq:] ^= 0x0F0F
+    y2 = O.attn_batch(q, k2, v2, n_kv_heads=hkv, n_ctx=nq + 5, q_base_pos=0)
+    assert np.array_equal(y, y2)
+
+
+# ------------------------------------------------------------ split-K partials/combine
+
+@pytest.mark.parametrize("chunk", [1, 7, 32, 128, 1000])
+def test_split_combine_equals_unsplit(chunk):
+    hq, hkv, hd, pos = 8, 2, 128, 900
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=pos + 1, seed=13)
+    n_chunks = (pos + 1 + chunk - 1) // chunk
+    part = O.split_partials(q, k, v, n_kv_heads=hkv, n_ctx=pos + 1, q_base_pos=pos, n_chunks=n_chunks, chunk=chunk)
+    y = O.split_combine(part).reshape(1, hq, hd)
+    r = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=pos + 1, q_base_pos=pos)
+    assert O.max_abs(y, r) < 2e-6 and O.rel_l2(y, r) < 1e-5
+
+
+def test_split_partials_causal_drafts():
+    """Speculative verify rows: drafts at q_base + i see keys <= q_base + i."""
+    hq, hkv, hd, base, nq = 8, 1, 256, 500, 4
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=14)
+    part = O.split_partials(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base, n_chunks=8, chunk=63)
+    y = O.split_combine(part).reshape(nq, hq, hd)
+    r = O.naive_f64(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base)
+    assert O.max_abs(y, r) < 1e-5
