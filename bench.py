@@ -137,6 +137,27 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False) -> dict:
     return res
 
 
+def copy_calibration(steps: int, warmup: int, nbytes: int = 256 << 20) -> None:
+    """A plain device-to-device copy of known size: the reference point that scales the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes nbytes)."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_()
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    s1.record()
+    s1.synchronize()
+    ms = s0.elapsed_time(s1) / steps
+    log(f"[bench] copy {nbytes >> 20} MiB: {ms * 1e3:.1f} us/launch, {2 * nbytes / (ms * 1e-3) / 1e9:.0f} GB/s "
+        f"(read+write), {nbytes / 1024:.0f} KiB read and written per launch")
+
+
 def cpu_baseline(target_s: float = 10.0) -> dict:
     """The reference's CPU prefill attention (attn_batch_cpu, restated in oracle/) timed on a
     bounded sample of the cfg2 workload: single thread (the reference's threading) plus an
@@ -194,8 +215,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=sorted(CONFIGS), default=None,
-                    help="measure one config only (for profiling runs)")
+    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy"], default=None,
+                    help="measure one config only (for profiling runs); 'copy' runs a plain "
+                         "device copy of 256 MiB that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -212,6 +234,9 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     log(f"[bench] device {props.name} CUs={props.multi_processor_count} lib={capi.version()}")
 
+    if args.only == "copy":
+        copy_calibration(args.steps, args.warmup)
+        return 0
     if args.only:
         measure(args.only, args.steps, args.warmup)
         return 0

@@ -177,8 +177,10 @@ def test_decode_split_count_invariance(hip):
     hq, hkv, hd, base = 16, 4, 128, 5000
     q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=base + 1, seed=8)
     outs = [run_decode(q, k, v, hkv=hkv, n_ctx=base + 1, q_base=base, n_splits=s) for s in (1, 3, 64, 157)]
+    # P is rounded to f16 relative to each split's own max, so split counts agree to the
+    # f16 rounding of P (2^-12 relative per term), not bit for bit.
     for o in outs[1:]:
-        assert O.max_abs(o, outs[0]) < 1e-5
+        assert O.max_abs(o, outs[0]) < 1e-4 and O.rel_l2(o, outs[0]) < 3e-4
 
 
 # ------------------------------------------------------------------ declines (device)
