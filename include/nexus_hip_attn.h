@@ -80,9 +80,12 @@ typedef struct nexus_attn_desc {
 /* Causal GQA flash-attention prefill over an f16 cache: cold prompts (q_base_pos = 0)
  * and prompt chunks appended after q_base_pos cached tokens.  Replaces
  * attention_flash_gpu / attention_batch_gpu / attention_stream_gpu
- * (src/gpu/vulkan_backend.h:584-608).  The workspace holds split-KV partials; pass
- * NULL/0 to run unsplit.  nexus_hip_attn_prefill_ws_bytes() returns the size that
- * enables the split the library would choose for this shape on this device. */
+ * (src/gpu/vulkan_backend.h:584-608).  The workspace lets the library split a long key
+ * range over several workgroups (its size comes from nexus_hip_attn_prefill_ws_bytes();
+ * NULL/0, or a smaller one, runs unsplit).  A handful of queries (n_query * G <= 32, e.g.
+ * speculative verify) runs through the split-KV decode kernel when the workspace allows.
+ * Workspace layout: f32 partials, then 8-byte arrival counters; it needs no
+ * initialisation and one workspace must not be shared by calls in flight at once. */
 int nexus_hip_attn_prefill(const nexus_attn_desc* desc,
                            const void* q, const uint16_t* k, const uint16_t* v, void* out,
                            void* workspace, size_t workspace_bytes,
@@ -93,9 +96,13 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc);
  * (n_query = 1 is ordinary decode, n_query > 1 is speculative/MTP verify with the
  * causal mask among the drafts).  Replaces attention_gpu (vulkan_backend.h:576-580)
  * and the attention core of q35_full_layer (part + comb, vulkan_backend.h:5462-5482).
- * partial_ws is f32 [n_query * n_q_heads][n_splits][head_dim + 2] holding, per split,
- * (sum_k e^{s_k - m} v_k, m, l) exactly as qwen35_attn_part.comp:3 defines them;
- * n_splits <= 0 lets the library choose.  Size from nexus_hip_attn_decode_ws_bytes(). */
+ * One launch: every split writes its partial and the last split of each (kv head, row
+ * group) to finish merges them and writes `out`.  partial_ws must hold
+ * nexus_hip_attn_decode_ws_bytes() bytes; it starts with f32
+ * [n_query * n_q_heads][n_splits][head_dim + 2] partials holding, per split,
+ * (sum_k e^{s_k - m} v_k, m, l) exactly as qwen35_attn_part.comp:3 defines them, followed
+ * (256-byte aligned) by the 8-byte arrival counters.  It needs no initialisation; calls
+ * in flight at once must not share it.  n_splits <= 0 lets the library choose. */
 int nexus_hip_attn_decode(const nexus_attn_desc* desc,
                           const void* q, const uint16_t* k, const uint16_t* v, void* out,
                           float* partial_ws, int n_splits,

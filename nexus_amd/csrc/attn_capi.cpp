@@ -9,6 +9,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -36,7 +37,16 @@ int ok()
 }
 
 constexpr int kMaxDevices = 64;
-constexpr int kMaxSplits = 1024;          // LSE combine holds one weight per split in LDS
+using nxa::kMaxSplits;
+
+// Launch epoch for the split-merge arrival counters (never 0, which marks a reset counter).
+uint32_t next_epoch()
+{
+    static std::atomic<uint32_t> g_epoch{0x5eed0001u};
+    uint32_t e = g_epoch.fetch_add(1u, std::memory_order_relaxed);
+    if (e == 0u) e = g_epoch.fetch_add(1u, std::memory_order_relaxed);
+    return e;
+}
 
 // Compute units of the current device (cached); 256 (MI355X) when no device is visible,
 // so workspace sizing is still defined on a host without a GPU.
@@ -75,6 +85,10 @@ int check_desc(const nexus_attn_desc* d)
         return fail(NEXUS_E_INVALID, "n_query=%d n_ctx=%d q_base_pos=%d", d->n_query, d->n_ctx, d->q_base_pos);
     if ((long long)d->q_base_pos + d->n_query > INT_MAX - 4096 || d->n_ctx > INT_MAX - 4096)
         return fail(NEXUS_E_UNSUPPORTED, "positions exceed the 31-bit range");
+    if ((long long)d->n_ctx * d->head_dim * 2 >= (1LL << 31))
+        return fail(NEXUS_E_UNSUPPORTED, "n_ctx * head_dim exceeds the 2 GiB per-kv-head buffer range");
+    if ((long long)d->n_query * d->n_q_heads * d->head_dim * 4 >= (1LL << 31))
+        return fail(NEXUS_E_UNSUPPORTED, "n_query * n_q_heads * head_dim exceeds the 2 GiB query buffer range");
     if (d->kv_row_stride < d->n_ctx)
         return fail(NEXUS_E_INVALID, "kv_row_stride=%lld < n_ctx=%d", (long long)d->kv_row_stride, d->n_ctx);
     if (d->sliding_window < 0) return fail(NEXUS_E_INVALID, "sliding_window=%d", d->sliding_window);
@@ -130,7 +144,19 @@ int default_decode_splits(const nexus_attn_desc* d)
 
 size_t decode_ws_bytes(const nexus_attn_desc* d, int n_splits)
 {
-    return (size_t)d->n_query * (size_t)d->n_q_heads * (size_t)n_splits * (size_t)(d->head_dim + 2) * sizeof(float);
+    return nxa::ws_total_bytes((long long)d->n_query * d->n_q_heads, n_splits, d->head_dim,
+                               (long long)d->n_kv_heads * decode_rowgroups(d));
+}
+
+long long prefill_qblocks(const nexus_attn_desc* d)
+{
+    return (d->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
+}
+
+size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
+{
+    return nxa::ws_total_bytes((long long)d->n_query * d->n_q_heads, splits, d->head_dim,
+                               prefill_qblocks(d) * d->n_q_heads);
 }
 
 // Split count of the prefill kernel: enough (query block, head, split) workgroups to fill
@@ -156,7 +182,7 @@ bool small_query_path(const nexus_attn_desc* d)
 }
 
 int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const uint16_t* v, void* out,
-               float* part, int n_splits, hipStream_t stream)
+               float* ws, int n_splits, hipStream_t stream)
 {
     int kb, ke;
     key_range(d, &kb, &ke);
@@ -164,12 +190,15 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     long long chunk = (kv_len + n_splits - 1) / n_splits;
     chunk = (chunk + nxa::kDecodeKeys - 1) / nxa::kDecodeKeys * nxa::kDecodeKeys;
     if (chunk < nxa::kDecodeKeys) chunk = nxa::kDecodeKeys;
+    const long long rows = (long long)d->n_query * d->n_q_heads;
 
     nxa::DecodeArgs a{};
     a.q = q;
     a.k = k;
     a.v = v;
-    a.part = part;
+    a.out = out;
+    a.part = ws;
+    a.counters = (unsigned long long*)((char*)ws + nxa::ws_counter_offset(rows, n_splits, d->head_dim));
     a.kv_stride = d->kv_row_stride;
     a.n_q_heads = d->n_q_heads;
     a.n_kv_heads = d->n_kv_heads;
@@ -186,16 +215,10 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.k_begin = kb;
     a.k_end = ke;
     a.n_rows = d->n_query * a.group;
-    hipError_t e = nxa::launch_decode(a, d->head_dim, d->q_dtype == NEXUS_DT_F32, is_ext(d),
-                                      decode_rowgroups(d), stream);
+    a.epoch = next_epoch();
+    hipError_t e = nxa::launch_decode(a, d->head_dim, d->q_dtype == NEXUS_DT_F32, d->o_dtype == NEXUS_DT_F32,
+                                      is_ext(d), decode_rowgroups(d), stream);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
-    nxa::CombineArgs c{};
-    c.part = part;
-    c.out = out;
-    c.n_rows = d->n_query * d->n_q_heads;
-    c.n_splits = n_splits;
-    e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
-    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
     return ok();
 }
 
@@ -236,7 +259,7 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
     if (small_query_path(desc)) return decode_ws_bytes(desc, default_decode_splits(desc));
     const int s = prefill_splits(desc);
     if (s <= 1) return 0;
-    return (size_t)desc->n_query * (size_t)desc->n_q_heads * (size_t)s * (size_t)(desc->head_dim + 2) * sizeof(float);
+    return prefill_split_ws_bytes(desc, s);
 }
 
 int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
@@ -257,9 +280,7 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     }
 
     int splits = prefill_splits(desc);
-    const size_t need = (size_t)desc->n_query * (size_t)desc->n_q_heads * (size_t)splits *
-                        (size_t)(desc->head_dim + 2) * sizeof(float);
-    if (splits > 1 && (!workspace || workspace_bytes < need)) splits = 1;
+    if (splits > 1 && (!workspace || workspace_bytes < prefill_split_ws_bytes(desc, splits))) splits = 1;
 
     nxa::PrefillArgs a{};
     a.q = q;
@@ -267,6 +288,10 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.v = v;
     a.out = out;
     a.part = (float*)workspace;
+    a.counters = splits > 1 ? (unsigned long long*)((char*)workspace +
+                                                    nxa::ws_counter_offset((long long)desc->n_query * desc->n_q_heads,
+                                                                           splits, desc->head_dim))
+                            : nullptr;
     a.kv_stride = desc->kv_row_stride;
     a.n_q_heads = desc->n_q_heads;
     a.n_kv_heads = desc->n_kv_heads;
@@ -278,23 +303,15 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.scale = eff_scale(desc);
     a.scale_log2 = a.scale * 1.4426950408889634f;
     a.softcap = desc->softcap;
-    a.n_qblocks = (desc->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
+    a.n_qblocks = (int)prefill_qblocks(desc);
     a.n_splits = splits;
+    a.epoch = next_epoch();
     const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
     if (items > INT_MAX) return fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
     hipError_t e = nxa::launch_prefill(a, desc->head_dim, desc->q_dtype == NEXUS_DT_F32,
                                        desc->o_dtype == NEXUS_DT_F32, is_ext(desc), s);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
-    if (splits > 1) {
-        nxa::CombineArgs c{};
-        c.part = (const float*)workspace;
-        c.out = out;
-        c.n_rows = desc->n_query * desc->n_q_heads;
-        c.n_splits = splits;
-        e = nxa::launch_combine(c, desc->head_dim, desc->o_dtype == NEXUS_DT_F32, s);
-        if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
-    }
     return ok();
 }
 

@@ -81,4 +81,43 @@ __device__ __forceinline__ int xcd_remap(int b, int n_items)
     return x * per + (x < rem ? x : rem) + t;
 }
 
+// ---- raw buffer loads: the descriptor's byte range makes out-of-range loads return 0,
+// so K/V rows past the cache end (or Q rows past n_query) need no branch.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;     // raw 32-bit dword buffer, gfx9 family
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t byte_off)
+{
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+
+// ---- split merge: the last of n workgroups to arrive combines the partials.
+// The 64-bit word holds (epoch << 32) | arrivals; a word whose epoch differs from this
+// launch's is stale (left by another launch or never initialised) and counts as zero.
+// The last arriver writes 0 back, so a graph replaying the same epoch starts clean.
+__device__ __forceinline__ bool arrive_is_last(unsigned long long* c, uint32_t epoch, uint32_t n)
+{
+    unsigned long long old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (true) {
+        const unsigned long long next = ((uint32_t)(old >> 32) == epoch)
+                                            ? old + 1ull
+                                            : (((unsigned long long)epoch << 32) | 1ull);
+        const unsigned long long prev = atomicCAS(c, old, next);
+        if (prev == old) return (uint32_t)next == n;
+        old = prev;
+    }
+}
+__device__ __forceinline__ void counter_reset(unsigned long long* c)
+{
+    __hip_atomic_store(c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Writers: make this thread's partial stores visible device-wide (L2 write-back only).
+__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+// Last arriver: see the other workgroups' partials (L2 invalidate only).
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
 }  // namespace nxa

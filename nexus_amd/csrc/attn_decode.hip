@@ -3,8 +3,9 @@
 // Pass 1 of the reference's decode split-K (src/gpu/shaders/qwen35_attn_part.comp:1-108):
 // one workgroup per (split, kv head, group of <= 32 query rows) writes, for every query
 // row, acc[hd] = sum_k e^{s_k - m} v_k, m (the split's max score) and l = sum_k e^{s_k - m}
-// to part[row][split][hd + 2] -- the reference's partial format.  Pass 2 is the LSE
-// combine in attn_prefill.hip (qwen35_attn_comb.comp:16-40).
+// to part[row][split][hd + 2] -- the reference's partial format.  The last workgroup of
+// a (kv head, row group) to finish merges all splits with the LSE rule of pass 2
+// (qwen35_attn_comb.comp:16-40, without the gate) and writes the output: one launch.
 //
 // Rows are (draft i, q head g of the GQA group) pairs, so every K/V byte a workgroup
 // reads is shared by all G heads of the group and all drafts of a speculative verify
@@ -47,7 +48,7 @@ __device__ __forceinline__ int dvt_off(int d, int c)
     return d * (kDecodeKeys * 2) + 16 * (c ^ ((d >> 2) & 3));
 }
 
-template <int HD, bool Q_F32, bool EXT>
+template <int HD, bool Q_F32, bool O_F32, bool EXT>
 __global__ void __launch_bounds__(kDecodeThreads, HD <= 128 ? 2 : 1)
 decode_kernel(DecodeArgs a)
 {
@@ -70,25 +71,25 @@ decode_kernel(DecodeArgs a)
     const int row_khi = min(qpos, a.n_ctx - 1);
 
     // ---- Q^T operands (f16 high part + f16 residual for f32 queries)
+    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
     f16x8 qhi[KSTEPS];
     f16x8 qlo[Q_F32 ? KSTEPS : 1];
     {
-        const size_t qoff = ((size_t)qi * a.n_q_heads + h) * HD + 8 * hh;
+        const rsrc_t qr = make_rsrc(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
+        // rows past n_rows point past the descriptor and read as zero
+        const uint32_t qoff = row_ok ? (uint32_t)((((size_t)qi * a.n_q_heads + h) * HD + 8 * hh) * QE) : 0x7fffff00u;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if constexpr (Q_F32) {
-                const f32x4* p = (const f32x4*)((const float*)a.q + qoff + 16 * ks);
-                f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
-                if (row_ok) { x0 = p[0]; x1 = p[1]; }
+                const f32x4 x0 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks));
+                const f32x4 x1 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks + 16));
                 const f16x8 hi = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
                 qhi[ks] = hi;
                 qlo[ks] = cvt_f16x8(x0[0] - (float)hi[0], x0[1] - (float)hi[1], x0[2] - (float)hi[2],
                                     x0[3] - (float)hi[3], x1[0] - (float)hi[4], x1[1] - (float)hi[5],
                                     x1[2] - (float)hi[6], x1[3] - (float)hi[7]);
             } else {
-                u32x4 x = {0u, 0u, 0u, 0u};
-                if (row_ok) x = *(const u32x4*)((const uint16_t*)a.q + qoff + 16 * ks);
-                qhi[ks] = as_f16x8(x);
+                qhi[ks] = as_f16x8(buf_load16(qr, qoff + 32 * ks));
             }
         }
     }
@@ -97,8 +98,10 @@ decode_kernel(DecodeArgs a)
     const int s_end = min(s_begin + a.chunk, a.k_end);
     const int n_sub = s_begin < s_end ? (s_end - s_begin + L::KEYS - 1) / L::KEYS : 0;
 
-    const uint16_t* kbase = a.k + (size_t)kvh * (size_t)a.kv_stride * HD;
-    const uint16_t* vbase = a.v + (size_t)kvh * (size_t)a.kv_stride * HD;
+    // K/V of this kv head; the descriptors end at this split's last key
+    const uint32_t kv_bytes = (uint32_t)max(s_end, 0) * HD * 2;
+    const rsrc_t krs = make_rsrc(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    const rsrc_t vrs = make_rsrc(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     uint8_t* vw = lds + wave * L::V_WAVE;
     const float fc = EXT ? 1.f : a.scale_log2;
 
@@ -114,15 +117,9 @@ decode_kernel(DecodeArgs a)
         // K rows -> A operands: lane (key n, k-group hh)
         f16x8 ka[KSTEPS];
         {
-            const int kr = key0 + n;
-            const bool ok = kr < s_end;
-            const uint16_t* kp = kbase + (size_t)kr * HD + 8 * hh;
+            const uint32_t koff = ((uint32_t)(key0 + n) * HD + 8 * hh) * 2;
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-                u32x4 x = {0u, 0u, 0u, 0u};
-                if (ok) x = *(const u32x4*)(kp + 16 * ks);
-                ka[ks] = as_f16x8(x);
-            }
+            for (int ks = 0; ks < KSTEPS; ++ks) ka[ks] = as_f16x8(buf_load16(krs, koff + 32 * ks));
         }
         // V rows -> registers: 4 consecutive keys x 8 dims per block
         u32x4 vr[L::V_LOADS][4];
@@ -131,12 +128,8 @@ decode_kernel(DecodeArgs a)
             const int blk = lane + 64 * i;
             const int kq = blk & 7, cc = blk >> 3;
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int gk = key0 + 4 * kq + r4;
-                u32x4 x = {0u, 0u, 0u, 0u};
-                if (gk < s_end) x = *(const u32x4*)(vbase + (size_t)gk * HD + 8 * cc);
-                vr[i][r4] = x;
-            }
+            for (int r4 = 0; r4 < 4; ++r4)
+                vr[i][r4] = buf_load16(vrs, ((uint32_t)(key0 + 4 * kq + r4) * HD + 8 * cc) * 2);
         }
         // S^T = K Q^T
         f32x16 s;
@@ -214,7 +207,7 @@ decode_kernel(DecodeArgs a)
         wave_lds_sync();
     }
 
-    // ---- merge the 4 waves' (m, l, O) in LDS, wave 0 writes the split partial
+    // ---- merge the 4 waves' (m, l, O) in LDS (log2 units)
     float l_tot = l + xor32(l);
     __syncthreads();                                       // V^T regions are reused below
     float* slot0 = (float*)lds;
@@ -239,75 +232,142 @@ decode_kernel(DecodeArgs a)
         l_tot = l_tot * c1 + l2 * c2;
         m = M;
     };
-    if (wave >= 2) put(wave == 2 ? slot0 : slot1);
-    __syncthreads();
-    if (wave < 2) take(wave == 0 ? slot0 : slot1);
-    __syncthreads();
-    if (wave == 1) put(slot0);
-    __syncthreads();
-    if (wave != 0) return;
-    take(slot0);
-    if (!row_ok) return;
+    auto merge_waves = [&]() {                             // result in wave 0
+        if (wave >= 2) put(wave == 2 ? slot0 : slot1);
+        __syncthreads();
+        if (wave < 2) take(wave == 0 ? slot0 : slot1);
+        __syncthreads();
+        if (wave == 1) put(slot0);
+        __syncthreads();
+        if (wave == 0) take(slot0);
+    };
+    auto store_out = [&]() {                               // wave 0: normalised output row
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        const size_t obase = ((size_t)qi * a.n_q_heads + h) * HD;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                const int dim = 32 * db + 8 * a4 + 4 * hh;
+                const float v0 = o[db][4 * a4] * inv, v1 = o[db][4 * a4 + 1] * inv;
+                const float v2 = o[db][4 * a4 + 2] * inv, v3 = o[db][4 * a4 + 3] * inv;
+                if constexpr (O_F32) {
+                    f32x4 x = {v0, v1, v2, v3};
+                    *(f32x4*)((float*)a.out + obase + dim) = x;
+                } else {
+                    f32x2 p0 = {v0, v1}, p1 = {v2, v3};
+                    f16x2 h0 = __builtin_convertvector(p0, f16x2);
+                    f16x2 h1 = __builtin_convertvector(p1, f16x2);
+                    u32x2 x = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
+                    *(u32x2*)((uint16_t*)a.out + obase + dim) = x;
+                }
+            }
+    };
+    merge_waves();
+    if (a.n_splits == 1) {
+        if (wave == 0 && row_ok) store_out();
+        return;
+    }
 
-    float* pr = a.part + (((size_t)qi * a.n_q_heads + h) * a.n_splits + split) * (HD + 2);
+    // ---- publish this split's partial; the last split to arrive merges all of them
+    const size_t prow = (size_t)qi * a.n_q_heads + h;
+    if (wave == 0 && row_ok) {
+        float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                const int dim = 32 * db + 8 * a4 + 4 * hh;
+                f32x2 x0 = {o[db][4 * a4], o[db][4 * a4 + 1]};
+                f32x2 x1 = {o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
+                *(f32x2*)(pr + dim) = x0;
+                *(f32x2*)(pr + dim + 2) = x1;
+            }
+        if (hh == 0) {
+            pr[HD] = m * kLn2;               // natural-log units, as qwen35_attn_part.comp stores m
+            pr[HD + 1] = l_tot;
+        }
+    }
+    release_agent();
+    __shared__ int s_last;
+    __syncthreads();
+    unsigned long long* cnt = a.counters + (size_t)kvh * gridDim.z + rg;
+    if (tid == 0) s_last = arrive_is_last(cnt, a.epoch, (uint32_t)a.n_splits);
+    __syncthreads();
+    if (!s_last) return;
+    acquire_agent();
+    // wave w folds splits w, w + 4, ... of its rows, then the 4 waves merge in LDS
+    m = kNegBig;
+    l_tot = 0.f;
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-            const int dim = 32 * db + 8 * a4 + 4 * hh;
-            f32x2 x0 = {o[db][4 * a4], o[db][4 * a4 + 1]};
-            f32x2 x1 = {o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
-            *(f32x2*)(pr + dim) = x0;
-            *(f32x2*)(pr + dim + 2) = x1;
+        for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
+    if (row_ok) {
+        for (int s2 = wave; s2 < a.n_splits; s2 += 4) {
+            const float* pr = a.part + (prow * a.n_splits + s2) * (HD + 2);
+            const float m2 = pr[HD] * kLog2e, l2 = pr[HD + 1];
+            const float M = fmaxf(m, m2);
+            const float c1 = fast_exp2(m - M), c2 = fast_exp2(m2 - M);
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    const int dim = 32 * db + 8 * a4 + 4 * hh;
+                    const f32x2 x0 = *(const f32x2*)(pr + dim);
+                    const f32x2 x1 = *(const f32x2*)(pr + dim + 2);
+                    o[db][4 * a4] = o[db][4 * a4] * c1 + x0[0] * c2;
+                    o[db][4 * a4 + 1] = o[db][4 * a4 + 1] * c1 + x0[1] * c2;
+                    o[db][4 * a4 + 2] = o[db][4 * a4 + 2] * c1 + x1[0] * c2;
+                    o[db][4 * a4 + 3] = o[db][4 * a4 + 3] * c1 + x1[1] * c2;
+                }
+            l_tot = l_tot * c1 + l2 * c2;
+            m = M;
         }
-    if (hh == 0) {
-        pr[HD] = m * kLn2;               // natural-log units, as qwen35_attn_part.comp stores m
-        pr[HD + 1] = l_tot;
     }
+    __syncthreads();
+    merge_waves();
+    if (wave == 0 && row_ok) store_out();
+    if (tid == 0) counter_reset(cnt);
 }
 
-size_t decode_lds_bytes(int head_dim)
-{
-    switch (head_dim) {
-    case 64: return DecodeLayout<64>::LDS_BYTES;
-    case 128: return DecodeLayout<128>::LDS_BYTES;
-    case 192: return DecodeLayout<192>::LDS_BYTES;
-    case 256: return DecodeLayout<256>::LDS_BYTES;
-    default: return 0;
-    }
-}
-
-template <int HD, bool QF, bool EXT>
+template <int HD, bool QF, bool OF, bool EXT>
 static hipError_t launch_decode_t(const DecodeArgs& a, int n_rowgroups, hipStream_t stream)
 {
     constexpr int lds_bytes = DecodeLayout<HD>::LDS_BYTES;
-    static bool attr_done = false;
+    static bool attr_done = false;        // set once per instantiation (idempotent)
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<HD, QF, EXT>,
+        hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<HD, QF, OF, EXT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    hipLaunchKernelGGL((decode_kernel<HD, QF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
+    hipLaunchKernelGGL((decode_kernel<HD, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
                        dim3(kDecodeThreads), lds_bytes, stream, a);
     return hipGetLastError();
 }
 
-template <int HD>
-static hipError_t launch_decode_hd(const DecodeArgs& a, bool q_f32, bool ext, int nrg, hipStream_t s)
+template <int HD, bool QF>
+static hipError_t launch_decode_q(const DecodeArgs& a, bool o_f32, bool ext, int nrg, hipStream_t s)
 {
-    if (ext) return q_f32 ? launch_decode_t<HD, true, true>(a, nrg, s) : launch_decode_t<HD, false, true>(a, nrg, s);
-    return q_f32 ? launch_decode_t<HD, true, false>(a, nrg, s) : launch_decode_t<HD, false, false>(a, nrg, s);
+    if (ext) return o_f32 ? launch_decode_t<HD, QF, true, true>(a, nrg, s) : launch_decode_t<HD, QF, false, true>(a, nrg, s);
+    return o_f32 ? launch_decode_t<HD, QF, true, false>(a, nrg, s) : launch_decode_t<HD, QF, false, false>(a, nrg, s);
 }
 
-hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool ext, int n_rowgroups,
-                         hipStream_t stream)
+template <int HD>
+static hipError_t launch_decode_hd(const DecodeArgs& a, bool q_f32, bool o_f32, bool ext, int nrg, hipStream_t s)
+{
+    return q_f32 ? launch_decode_q<HD, true>(a, o_f32, ext, nrg, s) : launch_decode_q<HD, false>(a, o_f32, ext, nrg, s);
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
+                         int n_rowgroups, hipStream_t stream)
 {
     switch (head_dim) {
-    case 64: return launch_decode_hd<64>(a, q_f32, ext, n_rowgroups, stream);
-    case 128: return launch_decode_hd<128>(a, q_f32, ext, n_rowgroups, stream);
-    case 192: return launch_decode_hd<192>(a, q_f32, ext, n_rowgroups, stream);
-    case 256: return launch_decode_hd<256>(a, q_f32, ext, n_rowgroups, stream);
+    case 64: return launch_decode_hd<64>(a, q_f32, o_f32, ext, n_rowgroups, stream);
+    case 128: return launch_decode_hd<128>(a, q_f32, o_f32, ext, n_rowgroups, stream);
+    case 192: return launch_decode_hd<192>(a, q_f32, o_f32, ext, n_rowgroups, stream);
+    case 256: return launch_decode_hd<256>(a, q_f32, o_f32, ext, n_rowgroups, stream);
     default: return hipErrorInvalidValue;
     }
 }

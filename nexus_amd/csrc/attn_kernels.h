@@ -1,4 +1,4 @@
-// nexus_amd/csrc/attn_kernels.h -- kernel argument blocks and launchers (host side).
+// nexus_amd/csrc/attn_kernels.h -- kernel argument blocks, workspace layout and launchers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -16,55 +16,65 @@ constexpr int kPrefillThreads = 256;
 constexpr int kDecodeThreads = 256;
 constexpr int kDecodeKeys = 32;
 constexpr int kDecodeRows = 32;
+constexpr int kMaxSplits = 1024;
 
 struct PrefillArgs {
     const void* q;
     const uint16_t* k;
     const uint16_t* v;
-    void* out;             // final output (n_splits == 1)
-    float* part;           // [n_query*Hq][n_splits][hd+2] partials (n_splits > 1)
-    long long kv_stride;   // tokens between kv heads
+    void* out;
+    float* part;                    // [n_query*Hq][n_splits][hd+2] partials (n_splits > 1)
+    unsigned long long* counters;   // [n_qblocks * Hq] arrival counters (n_splits > 1)
+    long long kv_stride;            // tokens between kv heads
     int n_q_heads, n_kv_heads, group;
     int n_query, q_base, n_ctx;
     int sliding_window;
-    float scale;           // natural-log scale applied to q.k
-    float scale_log2;      // scale * log2(e)
+    float scale;                    // natural-log scale applied to q.k
+    float scale_log2;               // scale * log2(e)
     float softcap;
     int n_qblocks, n_splits, n_items;
+    uint32_t epoch;
 };
 
 struct DecodeArgs {
     const void* q;
     const uint16_t* k;
     const uint16_t* v;
-    float* part;           // [n_query*Hq][n_splits][hd+2]
+    void* out;                      // [n_query][Hq][hd]
+    float* part;                    // [n_query*Hq][n_splits][hd+2]
+    unsigned long long* counters;   // [Hkv * n_rowgroups] arrival counters
     long long kv_stride;
     int n_q_heads, n_kv_heads, group;
     int n_query, q_base, n_ctx;
     int sliding_window;
     float scale, scale_log2, softcap;
     int n_splits;
-    int chunk;             // keys per split, multiple of kDecodeKeys
-    int k_begin;           // first key any row can see
-    int k_end;             // one past the last key any row can see
-    int n_rows;            // n_query * group
+    int chunk;                      // keys per split, multiple of kDecodeKeys
+    int k_begin;                    // first key any row can see
+    int k_end;                      // one past the last key any row can see
+    int n_rows;                     // n_query * group
+    uint32_t epoch;
 };
 
-struct CombineArgs {
-    const float* part;     // [n_rows][n_splits][hd+2]
-    void* out;             // [n_rows][hd], row = qi*Hq + h
-    int n_rows, n_splits;
-};
+// Workspace = f32 partials [rows][splits][hd+2] (the reference's split-K partial format,
+// qwen35_attn_part.comp:3) followed, 256-byte aligned, by one 8-byte counter per merge group.
+inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
+{
+    return (size_t)rows * (size_t)splits * (size_t)(head_dim + 2) * sizeof(float);
+}
+inline size_t ws_counter_offset(long long rows, int splits, int head_dim)
+{
+    return (ws_partial_bytes(rows, splits, head_dim) + 255) & ~(size_t)255;
+}
+inline size_t ws_total_bytes(long long rows, int splits, int head_dim, long long n_counters)
+{
+    return ws_counter_offset(rows, splits, head_dim) + (size_t)n_counters * 8;
+}
 
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.
 hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                           hipStream_t stream);
-hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool ext,
+hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);
-hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream);
-
-// Dynamic LDS bytes each kernel needs (host side, for validation and attributes).
-size_t prefill_lds_bytes(int head_dim);
-size_t decode_lds_bytes(int head_dim);
 
 }  // namespace nxa

@@ -19,8 +19,12 @@
 //    issued before the current tile's MFMAs, one barrier per tile.
 //  * Blocks are remapped so each XCD owns whole KV heads (L2 reuse of K/V), and within a
 //    KV head the heaviest (latest) query blocks start first.
+//  * K/V/Q come in through raw buffer loads whose descriptor ends at the cache end (or
+//    the last query), so rows past it read as zero with no branch in the loop.
 //  * Optional split of the key range over n_splits workgroups (short chunks over a long
-//    cache, e.g. 512 queries after 4096 cached tokens) with an fp32 LSE combine pass.
+//    cache, e.g. 512 queries after 4096 cached tokens).  Each split writes fp32 partials
+//    (acc, m, l); the last workgroup of a (query block, head) to arrive merges them with
+//    the LSE rule of qwen35_attn_comb.comp:16-40 and writes the output -- no second pass.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -105,53 +109,49 @@ prefill_kernel(PrefillArgs a)
         w_klo = a.q_base + w_first + 1 - a.sliding_window;
 
     // ---- Q^T operands: lane (query n, k-group hh) holds dims 16*ks + 8*hh .. +7
+    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
     f16x8 qt[KSTEPS];
     {
-        const size_t qoff = ((size_t)(row_ok ? qrow : 0) * a.n_q_heads + h) * HD + 8 * hh;
+        const size_t row_bytes = (size_t)a.n_q_heads * HD * QE;
+        const int blk_rows = min(BM, a.n_query - q0);
+        const rsrc_t qr = make_rsrc((const char*)a.q + (size_t)q0 * row_bytes, (uint32_t)(blk_rows * row_bytes));
+        const uint32_t qoff = (uint32_t)((32 * wave + n) * row_bytes + ((size_t)h * HD + 8 * hh) * QE);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if constexpr (Q_F32) {
-                const f32x4* p = (const f32x4*)((const float*)a.q + qoff + 16 * ks);
-                f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
-                if (row_ok) { x0 = p[0]; x1 = p[1]; }
+                const f32x4 x0 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks));
+                const f32x4 x1 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks + 16));
                 qt[ks] = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
             } else {
-                u32x4 x = {0u, 0u, 0u, 0u};
-                if (row_ok) x = *(const u32x4*)((const uint16_t*)a.q + qoff + 16 * ks);
-                qt[ks] = as_f16x8(x);
+                qt[ks] = as_f16x8(buf_load16(qr, qoff + 32 * ks));
             }
         }
     }
 
-    const uint16_t* kbase = a.k + (size_t)kvh * (size_t)a.kv_stride * HD;
-    const uint16_t* vbase = a.v + (size_t)kvh * (size_t)a.kv_stride * HD;
+    // K/V of this kv head; the descriptors end at row n_ctx
+    const uint32_t kv_bytes = (uint32_t)a.n_ctx * HD * 2;
+    const rsrc_t krs = make_rsrc(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    const rsrc_t vrs = make_rsrc(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     u32x4 kreg[L::K_LOADS];
     u32x4 vreg[L::V_LOADS][4];
 
-    // global -> registers for tile t (rows at or past n_ctx read as zero)
+    // global -> registers for tile t
     auto load_tile = [&](int t) {
-        const int key0 = t * BN;
+        const uint32_t key0 = (uint32_t)(t * BN);
 #pragma unroll
         for (int i = 0; i < L::K_LOADS; ++i) {
             const int idx = tid + kPrefillThreads * i;
             const int key = idx / L::CPR, c = idx % L::CPR;
-            const int gk = key0 + key;
-            u32x4 x = {0u, 0u, 0u, 0u};
-            if (gk < a.n_ctx) x = *(const u32x4*)(kbase + (size_t)gk * HD + 8 * c);
-            kreg[i] = x;
+            kreg[i] = buf_load16(krs, ((key0 + key) * HD + 8 * c) * 2);
         }
 #pragma unroll
         for (int j = 0; j < L::V_LOADS; ++j) {
             const int blk = tid + kPrefillThreads * j;
-            if (blk < L::V_BLOCKS) {
+            if (L::V_BLOCKS % kPrefillThreads == 0 || blk < L::V_BLOCKS) {
                 const int kq = blk & 15, cc = blk >> 4;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int gk = key0 + 4 * kq + i;
-                    u32x4 x = {0u, 0u, 0u, 0u};
-                    if (gk < a.n_ctx) x = *(const u32x4*)(vbase + (size_t)gk * HD + 8 * cc);
-                    vreg[j][i] = x;
-                }
+                for (int i = 0; i < 4; ++i)
+                    vreg[j][i] = buf_load16(vrs, ((key0 + 4 * kq + i) * HD + 8 * cc) * 2);
             }
         }
     };
@@ -168,7 +168,7 @@ prefill_kernel(PrefillArgs a)
 #pragma unroll
         for (int j = 0; j < L::V_LOADS; ++j) {
             const int blk = tid + kPrefillThreads * j;
-            if (blk < L::V_BLOCKS) {
+            if (L::V_BLOCKS % kPrefillThreads == 0 || blk < L::V_BLOCKS) {
                 const int kq = blk & 15, cc = blk >> 4;
                 const int q4 = kq & 3;
                 const int pos = ((q4 & 1) << 1) | (q4 >> 1);      // slot quad within the 16-key group
@@ -291,10 +291,8 @@ prefill_kernel(PrefillArgs a)
     }
 
     // ---- epilogue: lane (query n, hh) holds dims 32*db + 8*a4 + 4*hh + (0..3)
-    const float l_tot = l_part + xor32(l_part);
-    if (!row_ok) return;
-    if (a.n_splits == 1) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    float l_tot = l_part + xor32(l_part);
+    auto store_out = [&](float inv) {
         const size_t obase = ((size_t)qrow * a.n_q_heads + h) * HD;
 #pragma unroll
         for (int db = 0; db < DBLK; ++db)
@@ -314,8 +312,16 @@ prefill_kernel(PrefillArgs a)
                     *(u32x2*)((uint16_t*)a.out + obase + dim) = x;
                 }
             }
-    } else {
-        float* pr = a.part + (((size_t)qrow * a.n_q_heads + h) * a.n_splits + split) * (HD + 2);
+    };
+    if (a.n_splits == 1) {
+        if (row_ok) store_out(l_tot > 0.f ? 1.f / l_tot : 0.f);
+        return;
+    }
+
+    // ---- split-KV: publish this split's partial, the last arriver merges all of them
+    const size_t prow = (size_t)qrow * a.n_q_heads + h;
+    if (row_ok) {
+        float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
 #pragma unroll
         for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -327,71 +333,47 @@ prefill_kernel(PrefillArgs a)
                 *(f32x2*)(pr + dim + 2) = x1;
             }
         if (hh == 0) {
-            pr[HD] = m_used * kLn2;
+            pr[HD] = m_used * kLn2;          // natural-log units
             pr[HD + 1] = l_tot;
         }
     }
-}
-
-// ---- LSE combine of split partials (qwen35_attn_comb.comp:16-40 without the gate):
-// out = sum_c acc_c e^{m_c - M} / sum_c l_c e^{m_c - M}, zeros when the row saw no key.
-constexpr int kCombineThreads = 128;
-constexpr int kMaxSplits = 1024;
-
-template <int HD, bool O_F32>
-__global__ void __launch_bounds__(kCombineThreads)
-combine_kernel(CombineArgs a)
-{
-    __shared__ float wgt[kMaxSplits];
-    __shared__ float red[kCombineThreads];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
-
-    float mx = -3.0e38f;
-    for (int c = tid; c < a.n_splits; c += kCombineThreads) mx = fmaxf(mx, pr[(size_t)c * (HD + 2) + HD]);
-    red[tid] = mx;
+    release_agent();
+    __shared__ int s_last;
     __syncthreads();
-    for (int s = kCombineThreads / 2; s > 0; s >>= 1) {
-        if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-        __syncthreads();
-    }
-    const float M = red[0];
+    unsigned long long* cnt = a.counters + (size_t)qb * a.n_q_heads + h;
+    if (tid == 0) s_last = arrive_is_last(cnt, a.epoch, (uint32_t)a.n_splits);
     __syncthreads();
-    float lsum = 0.f;
-    for (int c = tid; c < a.n_splits; c += kCombineThreads) {
-        const float w = fast_exp2((pr[(size_t)c * (HD + 2) + HD] - M) * kLog2e);
-        wgt[c] = w;
-        lsum += w * pr[(size_t)c * (HD + 2) + HD + 1];
+    if (!s_last) return;
+    acquire_agent();
+    if (row_ok) {
+        float m_nat = m_used * kLn2;
+        for (int s2 = 0; s2 < a.n_splits; ++s2) {
+            if (s2 == split) continue;
+            const float* pr = a.part + (prow * a.n_splits + s2) * (HD + 2);
+            const float m2 = pr[HD], l2 = pr[HD + 1];
+            const float M = fmaxf(m_nat, m2);
+            const float c1 = fast_exp2((m_nat - M) * kLog2e), c2 = fast_exp2((m2 - M) * kLog2e);
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    const int dim = 32 * db + 8 * a4 + 4 * hh;
+                    const f32x2 x0 = *(const f32x2*)(pr + dim);
+                    const f32x2 x1 = *(const f32x2*)(pr + dim + 2);
+                    o[db][4 * a4] = o[db][4 * a4] * c1 + x0[0] * c2;
+                    o[db][4 * a4 + 1] = o[db][4 * a4 + 1] * c1 + x0[1] * c2;
+                    o[db][4 * a4 + 2] = o[db][4 * a4 + 2] * c1 + x1[0] * c2;
+                    o[db][4 * a4 + 3] = o[db][4 * a4 + 3] * c1 + x1[1] * c2;
+                }
+            l_tot = l_tot * c1 + l2 * c2;
+            m_nat = M;
+        }
+        store_out(l_tot > 0.f ? 1.f / l_tot : 0.f);
     }
-    red[tid] = lsum;
-    __syncthreads();
-    for (int s = kCombineThreads / 2; s > 0; s >>= 1) {
-        if (tid < s) red[tid] += red[tid + s];
-        __syncthreads();
-    }
-    const float Lsum = red[0];
-    const float inv = Lsum > 0.f ? 1.f / Lsum : 0.f;
-    for (int d = tid; d < HD; d += kCombineThreads) {
-        float acc = 0.f;
-        for (int c = 0; c < a.n_splits; ++c) acc += pr[(size_t)c * (HD + 2) + d] * wgt[c];
-        const float y = acc * inv;
-        if constexpr (O_F32) ((float*)a.out)[(size_t)row * HD + d] = y;
-        else ((_Float16*)a.out)[(size_t)row * HD + d] = (_Float16)y;
-    }
+    if (tid == 0) counter_reset(cnt);
 }
 
 // ---- launchers
-
-size_t prefill_lds_bytes(int head_dim)
-{
-    switch (head_dim) {
-    case 64: return PrefillLayout<64>::LDS_BYTES;
-    case 128: return PrefillLayout<128>::LDS_BYTES;
-    case 192: return PrefillLayout<192>::LDS_BYTES;
-    case 256: return PrefillLayout<256>::LDS_BYTES;
-    default: return 0;
-    }
-}
 
 template <int HD, bool QF, bool OF, bool EXT>
 static hipError_t launch_prefill_t(const PrefillArgs& a, hipStream_t stream)
@@ -428,25 +410,6 @@ hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o
     case 128: return launch_prefill_hd<128>(a, q_f32, o_f32, ext, stream);
     case 192: return launch_prefill_hd<192>(a, q_f32, o_f32, ext, stream);
     case 256: return launch_prefill_hd<256>(a, q_f32, o_f32, ext, stream);
-    default: return hipErrorInvalidValue;
-    }
-}
-
-template <int HD, bool OF>
-static hipError_t launch_combine_t(const CombineArgs& a, hipStream_t stream)
-{
-    hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows), dim3(kCombineThreads), 0, stream, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream)
-{
-    if (a.n_splits < 1 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
-    switch (head_dim) {
-    case 64: return o_f32 ? launch_combine_t<64, true>(a, stream) : launch_combine_t<64, false>(a, stream);
-    case 128: return o_f32 ? launch_combine_t<128, true>(a, stream) : launch_combine_t<128, false>(a, stream);
-    case 192: return o_f32 ? launch_combine_t<192, true>(a, stream) : launch_combine_t<192, false>(a, stream);
-    case 256: return o_f32 ? launch_combine_t<256, true>(a, stream) : launch_combine_t<256, false>(a, stream);
     default: return hipErrorInvalidValue;
     }
 }

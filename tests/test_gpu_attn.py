@@ -163,9 +163,10 @@ def test_decode_partials_have_reference_meaning(hip):
     n_ctx = base + 1
     splits = 8
     q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, n_ctx=n_ctx, seed=7)
-    ws = torch.zeros(hq * splits * (hd + 2), dtype=torch.float32, device="cuda")
+    desc = capi.make_desc(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=1, q_base_pos=base, n_ctx=n_ctx)
+    ws = torch.full((capi.decode_ws_bytes(desc, splits) // 4,), float("nan"), dtype=torch.float32, device="cuda")
     run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits, ws=ws)
-    got = ws.cpu().numpy().reshape(hq, splits, hd + 2)
+    got = ws[: hq * splits * (hd + 2)].cpu().numpy().reshape(hq, splits, hd + 2)
     chunk = ((n_ctx + splits - 1) // splits + 31) // 32 * 32
     ref = O.split_partials(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_chunks=splits, chunk=chunk)
     assert np.max(np.abs(got[:, :, hd] - ref[:, :, hd])) < 1e-4                     # m
