@@ -9,7 +9,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -38,15 +37,6 @@ int ok()
 
 constexpr int kMaxDevices = 64;
 using nxa::kMaxSplits;
-
-// Launch epoch for the split-merge arrival counters (never 0, which marks a reset counter).
-uint32_t next_epoch()
-{
-    static std::atomic<uint32_t> g_epoch{0x5eed0001u};
-    uint32_t e = g_epoch.fetch_add(1u, std::memory_order_relaxed);
-    if (e == 0u) e = g_epoch.fetch_add(1u, std::memory_order_relaxed);
-    return e;
-}
 
 // Compute units of the current device (cached); 256 (MI355X) when no device is visible,
 // so workspace sizing is still defined on a host without a GPU.
@@ -198,7 +188,7 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.v = v;
     a.out = out;
     a.part = ws;
-    a.counters = (unsigned long long*)((char*)ws + nxa::ws_counter_offset(rows, n_splits, d->head_dim));
+    a.counters = (unsigned int*)((char*)ws + nxa::ws_counter_offset(rows, n_splits, d->head_dim));
     a.kv_stride = d->kv_row_stride;
     a.n_q_heads = d->n_q_heads;
     a.n_kv_heads = d->n_kv_heads;
@@ -215,10 +205,23 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.k_begin = kb;
     a.k_end = ke;
     a.n_rows = d->n_query * a.group;
-    a.epoch = next_epoch();
+    // one workgroup folds rows_in_group x n_splits partials in the fused merge; a large
+    // fan-in goes to the combine kernel, which spreads it over (row, dim chunk) waves
+    const long long rows_in_group = std::min<long long>(a.n_rows, nxa::kDecodeRows);
+    const size_t merge_bytes = (size_t)rows_in_group * n_splits * (d->head_dim + 2) * sizeof(float);
+    a.fused_merge = (n_splits > 1 && merge_bytes <= nxa::kFusedMergeBytes) ? 1 : 0;
     hipError_t e = nxa::launch_decode(a, d->head_dim, d->q_dtype == NEXUS_DT_F32, d->o_dtype == NEXUS_DT_F32,
                                       is_ext(d), decode_rowgroups(d), stream);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
+    if (n_splits > 1 && !a.fused_merge) {
+        nxa::CombineArgs c{};
+        c.part = ws;
+        c.out = out;
+        c.n_rows = (int)rows;
+        c.n_splits = n_splits;
+        e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
+        if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
+    }
     return ok();
 }
 
@@ -288,7 +291,7 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.v = v;
     a.out = out;
     a.part = (float*)workspace;
-    a.counters = splits > 1 ? (unsigned long long*)((char*)workspace +
+    a.counters = splits > 1 ? (unsigned int*)((char*)workspace +
                                                     nxa::ws_counter_offset((long long)desc->n_query * desc->n_q_heads,
                                                                            splits, desc->head_dim))
                             : nullptr;
@@ -305,7 +308,6 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.softcap = desc->softcap;
     a.n_qblocks = (int)prefill_qblocks(desc);
     a.n_splits = splits;
-    a.epoch = next_epoch();
     const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
     if (items > INT_MAX) return fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;

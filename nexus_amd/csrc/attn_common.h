@@ -96,24 +96,16 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t byte_off)
 }
 
 // ---- split merge: the last of n workgroups to arrive combines the partials.
-// The 64-bit word holds (epoch << 32) | arrivals; a word whose epoch differs from this
-// launch's is stale (left by another launch or never initialised) and counts as zero.
-// The last arriver writes 0 back, so a graph replaying the same epoch starts clean.
-__device__ __forceinline__ bool arrive_is_last(unsigned long long* c, uint32_t epoch, uint32_t n)
+// One device-scope fetch-add per workgroup (no retry loop, so arrivals do not serialise
+// behind each other); the last arriver writes 0 back, leaving the counter ready for the
+// next launch or graph replay.  Counters must be zero before their first use.
+__device__ __forceinline__ bool arrive_is_last(unsigned int* c, unsigned int n)
 {
-    unsigned long long old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    while (true) {
-        const unsigned long long next = ((uint32_t)(old >> 32) == epoch)
-                                            ? old + 1ull
-                                            : (((unsigned long long)epoch << 32) | 1ull);
-        const unsigned long long prev = atomicCAS(c, old, next);
-        if (prev == old) return (uint32_t)next == n;
-        old = prev;
-    }
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1u;
 }
-__device__ __forceinline__ void counter_reset(unsigned long long* c)
+__device__ __forceinline__ void counter_reset(unsigned int* c)
 {
-    __hip_atomic_store(c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Writers: make this thread's partial stores visible device-wide (L2 write-back only).
 __device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }

@@ -291,8 +291,9 @@ decode_kernel(DecodeArgs a)
     release_agent();
     __shared__ int s_last;
     __syncthreads();
-    unsigned long long* cnt = a.counters + (size_t)kvh * gridDim.z + rg;
-    if (tid == 0) s_last = arrive_is_last(cnt, a.epoch, (uint32_t)a.n_splits);
+    if (!a.fused_merge) return;                            // a combine kernel follows
+    unsigned int* cnt = a.counters + (size_t)kvh * gridDim.z + rg;
+    if (tid == 0) s_last = arrive_is_last(cnt, (unsigned int)a.n_splits);
     __syncthreads();
     if (!s_last) return;
     acquire_agent();
@@ -329,6 +330,60 @@ decode_kernel(DecodeArgs a)
     merge_waves();
     if (wave == 0 && row_ok) store_out();
     if (tid == 0) counter_reset(cnt);
+}
+
+// ---- LSE combine for large fan-in (qwen35_attn_comb.comp:16-40 without the gate):
+// out[row][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, zeros for a row that
+// saw no key.  One wave per (row, 64-dim chunk); split weights are computed once per wave.
+constexpr int kCombineThreads = 64;
+
+template <int HD, bool O_F32>
+__global__ void __launch_bounds__(kCombineThreads)
+combine_kernel(CombineArgs a)
+{
+    __shared__ float wgt[kMaxSplits];
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const int d = blockIdx.y * kCombineThreads + lane;
+    const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
+    float mx = -3.0e38f;
+    for (int c = lane; c < a.n_splits; c += kCombineThreads) mx = fmaxf(mx, pr[(size_t)c * (HD + 2) + HD]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float lsum = 0.f;
+    for (int c = lane; c < a.n_splits; c += kCombineThreads) {
+        const float w = fast_exp2((pr[(size_t)c * (HD + 2) + HD] - mx) * kLog2e);
+        wgt[c] = w;
+        lsum += w * pr[(size_t)c * (HD + 2) + HD + 1];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
+    __syncthreads();
+    if (d >= HD) return;
+    float acc = 0.f;
+    for (int c = 0; c < a.n_splits; ++c) acc += pr[(size_t)c * (HD + 2) + d] * wgt[c];
+    const float y = lsum > 0.f ? acc / lsum : 0.f;
+    if constexpr (O_F32) ((float*)a.out)[(size_t)row * HD + d] = y;
+    else ((_Float16*)a.out)[(size_t)row * HD + d] = (_Float16)y;
+}
+
+template <int HD, bool OF>
+static hipError_t launch_combine_t(const CombineArgs& a, hipStream_t stream)
+{
+    hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows, (HD + kCombineThreads - 1) / kCombineThreads),
+                       dim3(kCombineThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream)
+{
+    if (a.n_splits < 1 || a.n_splits > kMaxSplits) return hipErrorInvalidValue;
+    switch (head_dim) {
+    case 64: return o_f32 ? launch_combine_t<64, true>(a, stream) : launch_combine_t<64, false>(a, stream);
+    case 128: return o_f32 ? launch_combine_t<128, true>(a, stream) : launch_combine_t<128, false>(a, stream);
+    case 192: return o_f32 ? launch_combine_t<192, true>(a, stream) : launch_combine_t<192, false>(a, stream);
+    case 256: return o_f32 ? launch_combine_t<256, true>(a, stream) : launch_combine_t<256, false>(a, stream);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 template <int HD, bool QF, bool OF, bool EXT>

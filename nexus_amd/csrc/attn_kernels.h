@@ -24,7 +24,7 @@ struct PrefillArgs {
     const uint16_t* v;
     void* out;
     float* part;                    // [n_query*Hq][n_splits][hd+2] partials (n_splits > 1)
-    unsigned long long* counters;   // [n_qblocks * Hq] arrival counters (n_splits > 1)
+    unsigned int* counters;         // [n_qblocks * Hq] arrival counters (n_splits > 1)
     long long kv_stride;            // tokens between kv heads
     int n_q_heads, n_kv_heads, group;
     int n_query, q_base, n_ctx;
@@ -33,7 +33,6 @@ struct PrefillArgs {
     float scale_log2;               // scale * log2(e)
     float softcap;
     int n_qblocks, n_splits, n_items;
-    uint32_t epoch;
 };
 
 struct DecodeArgs {
@@ -42,7 +41,7 @@ struct DecodeArgs {
     const uint16_t* v;
     void* out;                      // [n_query][Hq][hd]
     float* part;                    // [n_query*Hq][n_splits][hd+2]
-    unsigned long long* counters;   // [Hkv * n_rowgroups] arrival counters
+    unsigned int* counters;         // [Hkv * n_rowgroups] arrival counters (fused merge)
     long long kv_stride;
     int n_q_heads, n_kv_heads, group;
     int n_query, q_base, n_ctx;
@@ -53,11 +52,18 @@ struct DecodeArgs {
     int k_begin;                    // first key any row can see
     int k_end;                      // one past the last key any row can see
     int n_rows;                     // n_query * group
-    uint32_t epoch;
+    int fused_merge;                // 1: last split merges; 0: combine kernel follows
+};
+
+struct CombineArgs {
+    const float* part;              // [n_rows][n_splits][hd+2]
+    void* out;                      // [n_rows][hd], row = qi*Hq + h
+    int n_rows, n_splits;
 };
 
 // Workspace = f32 partials [rows][splits][hd+2] (the reference's split-K partial format,
-// qwen35_attn_part.comp:3) followed, 256-byte aligned, by one 8-byte counter per merge group.
+// qwen35_attn_part.comp:3) followed, 256-byte aligned, by one 4-byte counter per merge
+// group (8 bytes reserved per group).  Counters start at zero and are left at zero.
 inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
 {
     return (size_t)rows * (size_t)splits * (size_t)(head_dim + 2) * sizeof(float);
@@ -76,5 +82,10 @@ hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o
                           hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);
+hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream);
+
+// Largest partial volume (bytes) one merging workgroup folds in the fused merge; beyond it
+// a separate combine kernel spreads the merge over (row, dim-chunk) workgroups.
+constexpr size_t kFusedMergeBytes = 256u << 10;
 
 }  // namespace nxa

@@ -340,15 +340,20 @@ prefill_kernel(PrefillArgs a)
     release_agent();
     __shared__ int s_last;
     __syncthreads();
-    unsigned long long* cnt = a.counters + (size_t)qb * a.n_q_heads + h;
-    if (tid == 0) s_last = arrive_is_last(cnt, a.epoch, (uint32_t)a.n_splits);
+    unsigned int* cnt = a.counters + (size_t)qb * a.n_q_heads + h;
+    if (tid == 0) s_last = arrive_is_last(cnt, (unsigned int)a.n_splits);
     __syncthreads();
     if (!s_last) return;
     acquire_agent();
     if (row_ok) {
-        float m_nat = m_used * kLn2;
+        // fold splits 0..n-1 in index order, so the result does not depend on arrival order
+        float m_nat = kNegBig;
+        l_tot = 0.f;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
         for (int s2 = 0; s2 < a.n_splits; ++s2) {
-            if (s2 == split) continue;
             const float* pr = a.part + (prow * a.n_splits + s2) * (HD + 2);
             const float m2 = pr[HD], l2 = pr[HD + 1];
             const float M = fmaxf(m_nat, m2);
