@@ -1,0 +1,126 @@
+// nexus_amd/host/hip_attn_backend.h -- the engine-side attention backend for one MI355X.
+//
+// HipAttnBackend keeps the attention member functions of the reference's GPU backend
+// with their exact signatures and meaning, so the engine's call sites switch by changing
+// the object they call:
+//   attention_gpu         src/gpu/vulkan_backend.h:576-580  (impl :3731-3817)
+//   attention_batch_gpu   src/gpu/vulkan_backend.h:584-588  (impl :3819-3934)
+//   attention_stream_gpu  src/gpu/vulkan_backend.h:594-599  (impl :4085-4257)
+//   attention_flash_gpu   src/gpu/vulkan_backend.h:604-608  (impl :4260-4408)
+// and the callers in src/model/transformer.h:8478-8494 (prefill) and :11052 (decode).
+//
+// Contract carried over from the reference:
+//  * host pointers in and out: Q f32 [n_query][Hq][hd], K/V f16 [Hkv][n_ctx][hd] (the
+//    layout KVCache::pack_k/pack_v writes, src/model/kvcache.h:655-672), out f32;
+//  * synchronous: the call returns after the output is in host memory;
+//  * `return false` BEFORE any side effect when the call cannot run (unsupported shape,
+//    no device, allocation failure, disabled by NEXUS_ATTN_NOFLASH / NEXUS_FLASH_KV_MB),
+//    each distinct reason printed once to stderr like nx_decline (vulkan_backend.h:187-192);
+//    the caller then runs its CPU attention.
+// What changes: the kernels are the HIP ones behind include/nexus_hip_attn.h, the staging
+// buffers are device memory owned by the backend (grown, never shrunk), and the
+// device-resident entry points below skip the host round trip entirely.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+#include "nexus_hip_attn.h"
+
+namespace nexus {
+namespace hip {
+
+class HipAttnBackend {
+public:
+    HipAttnBackend() = default;
+    ~HipAttnBackend();
+    HipAttnBackend(const HipAttnBackend&) = delete;
+    HipAttnBackend& operator=(const HipAttnBackend&) = delete;
+
+    // Bind to a HIP device and create the backend's stream (default priority).  Returns
+    // false when no device is usable; every entry point then declines.
+    bool init(int device = 0);
+    bool ready() const { return ready_; }
+    int device() const { return device_; }
+
+    // ---- the reference's member functions (host pointers, synchronous) ----
+
+    // Decode of one token that sees all n_ctx keys; scale 1/sqrt(head_dim) as the
+    // reference's push constants set it (vulkan_backend.h:3785-3789).  `layer` is unused,
+    // as in the reference.  kv_bytes = bytes of one of K/V.
+    bool attention_gpu(const float* q, float* out,
+                       int n_heads, int n_kv_heads, int head_dim,
+                       int layer, int n_ctx,
+                       const void* k_flat, const void* v_flat,
+                       size_t kv_bytes);
+
+    // Batched prefill: query i at absolute position q_base_pos + i, causal, optional
+    // sliding window and softcap; scale 0 means 1/sqrt(head_dim).
+    bool attention_batch_gpu(const float* q_batch, float* out_batch,
+                             int n_q_heads, int n_kv_heads, int head_dim,
+                             int n_ctx, int n_query, int q_base_pos, int sliding_window,
+                             float scale, float softcap,
+                             const void* k_flat, const void* v_flat, size_t kv_bytes);
+
+    // Same results as attention_batch_gpu with no sliding window.  The reference streams
+    // K/V through a small device buffer in chunk_tokens pieces because its cards are short
+    // of memory; one MI355X holds any cache this entry point can be handed, so the whole
+    // K/V is staged once and chunk_tokens (>= 0) is accepted and not needed.
+    bool attention_stream_gpu(const float* q_batch, float* out_batch,
+                              int n_q_heads, int n_kv_heads, int head_dim,
+                              int n_ctx, int n_query, int q_base_pos,
+                              float scale, float softcap,
+                              const void* k_flat, const void* v_flat,
+                              int chunk_tokens);
+
+    // Tiled causal prompt attention (the engine's first choice for prefill).  Declines
+    // like the reference: NEXUS_ATTN_NOFLASH set, head_dim % 64 != 0 or > 256,
+    // Hq % Hkv != 0, null pointers, or 2 * K bytes above NEXUS_FLASH_KV_MB when that
+    // variable is set (unset: no limit, the cache lives in 288 GB of HBM).
+    bool attention_flash_gpu(const float* q_batch, float* out_batch,
+                             int n_q_heads, int n_kv_heads, int head_dim,
+                             int n_ctx, int n_query, int q_base_pos, int sliding_window,
+                             float scale, float softcap,
+                             const void* k_flat, const void* v_flat);
+
+    // ---- device-resident forms (device pointers, stream-ordered, no host copies) ----
+    // The workspace is the backend's own (one call in flight per backend at a time).
+    bool prefill_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
+                        const uint16_t* v, void* out, nexus_stream_t stream);
+    bool decode_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
+                       const uint16_t* v, void* out, int n_splits, nexus_stream_t stream);
+
+    // Counters for tests and logs.
+    long long calls_run() const { return calls_run_; }
+    long long calls_declined() const { return calls_declined_; }
+    const char* last_decline() const { return last_decline_; }
+
+private:
+    struct DevBuf {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    bool decline(const char* why);
+    bool ensure(DevBuf& b, size_t bytes, bool zero);
+    // Shared body of the host-pointer entry points: stage, run, copy back, wait.
+    bool run_host(const nexus_attn_desc& d, const float* q, const void* k_flat,
+                  const void* v_flat, float* out, bool decode);
+    bool run_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
+                    const uint16_t* v, void* out, int n_splits, bool decode, void* stream);
+
+    std::mutex mu_;
+    bool ready_ = false;
+    int device_ = -1;
+    void* stream_ = nullptr;                 // hipStream_t
+    DevBuf q_, k_, v_, o_, ws_;
+    long long calls_run_ = 0, calls_declined_ = 0;
+    const char* last_decline_ = "";
+};
+
+// Process-wide backend bound to device 0 on first use (the reference's gpu::gpu()
+// singleton, vulkan_backend.h:6079-6082).
+HipAttnBackend& backend();
+
+}  // namespace hip
+}  // namespace nexus
