@@ -82,11 +82,11 @@ typedef struct nexus_attn_desc {
  * attention_flash_gpu / attention_batch_gpu / attention_stream_gpu
  * (src/gpu/vulkan_backend.h:584-608).  The workspace lets the library split a long key
  * range over several workgroups (its size comes from nexus_hip_attn_prefill_ws_bytes();
- * NULL/0, or a smaller one, runs unsplit).  A handful of queries (n_query * G <= 32, e.g.
- * speculative verify) runs through the split-KV decode kernel when the workspace allows.
- * Workspace layout: f32 partials, then arrival counters.  Zero the whole workspace once
- * after allocating it; every call leaves the counters at zero again.  One workspace must
- * not be shared by calls in flight at once. */
+ * NULL/0, or a smaller one, runs unsplit); split partials are merged by a second launch
+ * on the same stream.  A handful of queries (n_query * G <= 32, e.g. speculative verify)
+ * runs through the split-KV decode kernels when the workspace allows.  The workspace
+ * holds f32 partials only and carries no state between calls (no zeroing needed); calls
+ * in flight at once must not share it. */
 int nexus_hip_attn_prefill(const nexus_attn_desc* desc,
                            const void* q, const uint16_t* k, const uint16_t* v, void* out,
                            void* workspace, size_t workspace_bytes,
@@ -97,14 +97,13 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc);
  * (n_query = 1 is ordinary decode, n_query > 1 is speculative/MTP verify with the
  * causal mask among the drafts).  Replaces attention_gpu (vulkan_backend.h:576-580)
  * and the attention core of q35_full_layer (part + comb, vulkan_backend.h:5462-5482).
- * Every split writes its partial; the last split of each (kv head, row group) to finish
- * merges them and writes `out` in the same launch (a large fan-in adds one parallel
- * combine launch instead).  partial_ws must hold nexus_hip_attn_decode_ws_bytes() bytes;
- * it starts with f32 [n_query * n_q_heads][n_splits][head_dim + 2] partials holding, per
- * split, (sum_k e^{s_k - m} v_k, m, l) exactly as qwen35_attn_part.comp:3 defines them,
- * followed (256-byte aligned) by the arrival counters.  Zero it once after allocating
- * it; every call leaves the counters at zero again.  Calls in flight at once must not
- * share it.  n_splits <= 0 lets the library choose. */
+ * Two launches on `stream`, like the reference's part + comb: every split writes its
+ * partial, then the combine merges them (one split writes `out` directly).  partial_ws
+ * must hold nexus_hip_attn_decode_ws_bytes() bytes: f32
+ * [n_query * n_q_heads][n_splits][head_dim + 2] partials holding, per split,
+ * (sum_k e^{s_k - m} v_k, m, l) exactly as qwen35_attn_part.comp:3 defines them.  It
+ * carries no state between calls; calls in flight at once must not share it.
+ * n_splits <= 0 lets the library choose. */
 int nexus_hip_attn_decode(const nexus_attn_desc* desc,
                           const void* q, const uint16_t* k, const uint16_t* v, void* out,
                           float* partial_ws, int n_splits,

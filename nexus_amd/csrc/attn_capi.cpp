@@ -110,10 +110,28 @@ void key_range(const nexus_attn_desc* d, int* k_begin, int* k_end)
     *k_end = (int)e;
 }
 
+long long decode_rows(const nexus_attn_desc* d)
+{
+    return (long long)d->n_query * (d->n_q_heads / d->n_kv_heads);
+}
+
+// 16-row tiles per workgroup: two when the rows need more than one tile, so a 32-row
+// verify batch (4 drafts x 8 heads) shares every K/V byte it reads.
+int decode_row_tiles(const nexus_attn_desc* d)
+{
+    return decode_rows(d) > nxa::kDecodeRowTile ? nxa::kDecodeMaxRowTiles : 1;
+}
+
 int decode_rowgroups(const nexus_attn_desc* d)
 {
-    const long long rows = (long long)d->n_query * (d->n_q_heads / d->n_kv_heads);
-    return (int)((rows + nxa::kDecodeRows - 1) / nxa::kDecodeRows);
+    const long long per = (long long)nxa::kDecodeRowTile * decode_row_tiles(d);
+    return (int)((decode_rows(d) + per - 1) / per);
+}
+
+// Workgroups resident at once per CU for the decode kernel (its register budget).
+int decode_wg_per_cu(const nexus_attn_desc* d)
+{
+    return d->head_dim * decode_row_tiles(d) <= 128 ? 2 : 1;     // decode_waves_per_simd
 }
 
 int default_decode_splits(const nexus_attn_desc* d)
@@ -122,10 +140,10 @@ int default_decode_splits(const nexus_attn_desc* d)
     key_range(d, &kb, &ke);
     const long long kv_len = ke - kb;
     const long long base = (long long)d->n_kv_heads * decode_rowgroups(d);
-    const long long target = 2LL * device_cus();
+    const long long target = (long long)decode_wg_per_cu(d) * device_cus();
     long long s = target / base;
     if (s < 1) s = 1;
-    const long long by_len = (kv_len + 127) / 128;           // keep >= 128 keys per split
+    const long long by_len = (kv_len + 127) / 128;           // keep >= 128 keys (one step per wave)
     if (s > by_len) s = by_len;
     if (s < 1) s = 1;
     if (s > kMaxSplits) s = kMaxSplits;
@@ -134,8 +152,7 @@ int default_decode_splits(const nexus_attn_desc* d)
 
 size_t decode_ws_bytes(const nexus_attn_desc* d, int n_splits)
 {
-    return nxa::ws_total_bytes((long long)d->n_query * d->n_q_heads, n_splits, d->head_dim,
-                               (long long)d->n_kv_heads * decode_rowgroups(d));
+    return nxa::ws_partial_bytes((long long)d->n_query * d->n_q_heads, n_splits, d->head_dim);
 }
 
 long long prefill_qblocks(const nexus_attn_desc* d)
@@ -145,8 +162,7 @@ long long prefill_qblocks(const nexus_attn_desc* d)
 
 size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
 {
-    return nxa::ws_total_bytes((long long)d->n_query * d->n_q_heads, splits, d->head_dim,
-                               prefill_qblocks(d) * d->n_q_heads);
+    return nxa::ws_partial_bytes((long long)d->n_query * d->n_q_heads, splits, d->head_dim);
 }
 
 // Split count of the prefill kernel: enough (query block, head, split) workgroups to fill
@@ -168,7 +184,19 @@ int prefill_splits(const nexus_attn_desc* d)
 
 bool small_query_path(const nexus_attn_desc* d)
 {
-    return (long long)d->n_query * (d->n_q_heads / d->n_kv_heads) <= nxa::kDecodeRows;
+    return decode_rows(d) <= (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
+}
+
+int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, int n_splits, hipStream_t stream)
+{
+    nxa::CombineArgs c{};
+    c.part = ws;
+    c.out = out;
+    c.n_rows = d->n_query * d->n_q_heads;
+    c.n_splits = n_splits;
+    const hipError_t e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
+    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
+    return NEXUS_OK;
 }
 
 int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const uint16_t* v, void* out,
@@ -180,7 +208,6 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     long long chunk = (kv_len + n_splits - 1) / n_splits;
     chunk = (chunk + nxa::kDecodeKeys - 1) / nxa::kDecodeKeys * nxa::kDecodeKeys;
     if (chunk < nxa::kDecodeKeys) chunk = nxa::kDecodeKeys;
-    const long long rows = (long long)d->n_query * d->n_q_heads;
 
     nxa::DecodeArgs a{};
     a.q = q;
@@ -188,7 +215,6 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.v = v;
     a.out = out;
     a.part = ws;
-    a.counters = (unsigned int*)((char*)ws + nxa::ws_counter_offset(rows, n_splits, d->head_dim));
     a.kv_stride = d->kv_row_stride;
     a.n_q_heads = d->n_q_heads;
     a.n_kv_heads = d->n_kv_heads;
@@ -204,23 +230,14 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.chunk = (int)chunk;
     a.k_begin = kb;
     a.k_end = ke;
-    a.n_rows = d->n_query * a.group;
-    // one workgroup folds rows_in_group x n_splits partials in the fused merge; a large
-    // fan-in goes to the combine kernel, which spreads it over (row, dim chunk) waves
-    const long long rows_in_group = std::min<long long>(a.n_rows, nxa::kDecodeRows);
-    const size_t merge_bytes = (size_t)rows_in_group * n_splits * (d->head_dim + 2) * sizeof(float);
-    a.fused_merge = (n_splits > 1 && merge_bytes <= nxa::kFusedMergeBytes) ? 1 : 0;
+    a.n_rows = (int)decode_rows(d);
+    a.row_tiles = decode_row_tiles(d);
     hipError_t e = nxa::launch_decode(a, d->head_dim, d->q_dtype == NEXUS_DT_F32, d->o_dtype == NEXUS_DT_F32,
                                       is_ext(d), decode_rowgroups(d), stream);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
-    if (n_splits > 1 && !a.fused_merge) {
-        nxa::CombineArgs c{};
-        c.part = ws;
-        c.out = out;
-        c.n_rows = (int)rows;
-        c.n_splits = n_splits;
-        e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
-        if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
+    if (n_splits > 1) {
+        const int rc = launch_combine_for(d, ws, out, n_splits, stream);
+        if (rc != NEXUS_OK) return rc;
     }
     return ok();
 }
@@ -291,10 +308,6 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.v = v;
     a.out = out;
     a.part = (float*)workspace;
-    a.counters = splits > 1 ? (unsigned int*)((char*)workspace +
-                                                    nxa::ws_counter_offset((long long)desc->n_query * desc->n_q_heads,
-                                                                           splits, desc->head_dim))
-                            : nullptr;
     a.kv_stride = desc->kv_row_stride;
     a.n_q_heads = desc->n_q_heads;
     a.n_kv_heads = desc->n_kv_heads;
@@ -314,6 +327,10 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     hipError_t e = nxa::launch_prefill(a, desc->head_dim, desc->q_dtype == NEXUS_DT_F32,
                                        desc->o_dtype == NEXUS_DT_F32, is_ext(desc), s);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
+    if (splits > 1) {
+        const int rc2 = launch_combine_for(desc, (float*)workspace, out, splits, s);
+        if (rc2 != NEXUS_OK) return rc2;
+    }
     return ok();
 }
 

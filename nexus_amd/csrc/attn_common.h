@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace nxa {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -31,6 +33,16 @@ constexpr float kRescaleThresh = 8.0f;
 __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// D = A(16x32) * B(32x16) + C, f16 inputs, f32 accumulate (v_mfma_f32_16x16x32_f16).
+// Lane l supplies A row (l & 15) and B column (l & 15), each with 8 k-values of k-group
+// (l >> 4); A and B assign k-values to register slots the same way, so any consistent
+// mapping of real indices to (group, slot) yields the full dot product.
+// D: lane l holds column (l & 15), rows 4*(l >> 4) + (0..3).
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 x) { return __builtin_bit_cast(f16x8, x); }
@@ -94,22 +106,5 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t byte_off)
 {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
 }
-
-// ---- split merge: the last of n workgroups to arrive combines the partials.
-// One device-scope fetch-add per workgroup (no retry loop, so arrivals do not serialise
-// behind each other); the last arriver writes 0 back, leaving the counter ready for the
-// next launch or graph replay.  Counters must be zero before their first use.
-__device__ __forceinline__ bool arrive_is_last(unsigned int* c, unsigned int n)
-{
-    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1u;
-}
-__device__ __forceinline__ void counter_reset(unsigned int* c)
-{
-    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Writers: make this thread's partial stores visible device-wide (L2 write-back only).
-__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-// Last arriver: see the other workgroups' partials (L2 invalidate only).
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 
 }  // namespace nxa

@@ -1,376 +1,489 @@
 // nexus_amd/csrc/attn_decode.hip -- split-KV ("flash decoding") attention for gfx950.
 //
-// Pass 1 of the reference's decode split-K (src/gpu/shaders/qwen35_attn_part.comp:1-108):
-// one workgroup per (split, kv head, group of <= 32 query rows) writes, for every query
-// row, acc[hd] = sum_k e^{s_k - m} v_k, m (the split's max score) and l = sum_k e^{s_k - m}
-// to part[row][split][hd + 2] -- the reference's partial format.  The last workgroup of
-// a (kv head, row group) to finish merges all splits with the LSE rule of pass 2
-// (qwen35_attn_comb.comp:16-40, without the gate) and writes the output: one launch.
+// Two passes, as the reference's decode split-K (src/gpu/shaders/qwen35_attn_part.comp and
+// qwen35_attn_comb.comp, dispatched back to back at src/gpu/vulkan_backend.h:5462-5482):
+//  * decode_part_kernel: one workgroup per (split, kv head, row group) streams its slice of
+//    the cache once and writes, for every query row, acc[hd] = sum_k e^{s_k - m} v_k,
+//    m (the split's max scaled score) and l = sum_k e^{s_k - m} to
+//    part[row][split][hd + 2] -- the reference's partial format (qwen35_attn_part.comp:3).
+//    With one split it writes the normalised output directly.
+//  * combine_kernel: out = sum_c acc_c e^{m_c - M} / sum_c l_c e^{m_c - M}, M = max_c m_c
+//    (qwen35_attn_comb.comp:16-40, without the output gate).
+// The kernel boundary makes the partials visible to the combine; an in-kernel
+// "last workgroup merges" scheme needs an agent-scope release per workgroup, which
+// writes back the XCD's L2 each time and measured slower than the second launch.
 //
-// Rows are (draft i, q head g of the GQA group) pairs, so every K/V byte a workgroup
-// reads is shared by all G heads of the group and all drafts of a speculative verify
-// (the reference's part kernel shares K/V rows across the G heads the same way).
+// Rows are (draft i, q head g of the GQA group) pairs, row = i * G + g, so every K/V byte a
+// workgroup reads feeds all G heads of the group and all drafts of a speculative verify.
 //
-// Per wave and 32-key step:
-//  * K rows go straight from HBM into MFMA A-operand registers (16-byte loads,
-//    lane = (key, half of a 16-dim slice)): no LDS round trip for K.
-//  * S^T = K Q^T on v_mfma_f32_32x32x16_f16.  f32 queries are split into an f16 high
-//    part and an f16 residual (two MFMAs), so scores carry ~22 mantissa bits like the
-//    reference's f32 dot products.  Causal mask among drafts (key <= q_base + i).
-//  * Exact online softmax (row max via one lane ^ 32 exchange), exp2 with log2(e) folded.
-//  * V is staged into a wave-private LDS region transposed (v_perm) and key-permuted so
-//    that P^T from the S^T registers feeds O^T += V^T P^T without shuffles.
-//  * The 4 waves of a workgroup take interleaved 32-key steps of the split and merge
-//    their (m, l, O) in LDS at the end.
+// Per wave and 32-key step (4 waves take interleaved steps of the split):
+//  * K rows go from HBM straight into MFMA A-operand registers (non-temporal 16-byte
+//    buffer loads, 64 contiguous bytes per key per instruction).  S^T = K Q^T on
+//    v_mfma_f32_16x16x32_f16, 16 query rows per row tile (RT tiles per wave).  f32
+//    queries are split into an f16 high part and an f16 residual (two MFMAs), so scores
+//    carry ~22 mantissa bits like the reference's f32 dot products.
+//  * The 32 keys of a step form two 16-key S^T tiles whose rows are the keys
+//    8*(r/4) + 4*t + (r%4) (tile t, row r).  The D layout then leaves lane (row n, group g)
+//    holding keys 8g..8g+7 of row n -- exactly the B operand of O^T += V^T P^T, so P
+//    needs no shuffle.  Row max/sum: two cross-lane exchanges (lane ^ 16, lane ^ 32).
+//  * V rows are transposed into a wave-private LDS region (v_perm, 8-byte writes) and read
+//    back as V^T A operands (16 bytes = 8 keys of one dim).
+//  * Software pipeline over register double buffers: K and V of step s + 2 are issued as
+//    soon as step s has consumed its K and V registers, so two steps (32 KB at hd 128) stay
+//    in flight per wave (one step for the largest tiles, hd x rows > 256).  The Q^T
+//    operands (f16 high/low parts) sit in LDS, one copy per workgroup, which keeps the
+//    register budget at two waves per SIMD for hd 128.
+//  * The 4 waves merge their (m, l, O) through LDS before the partial is written.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
 namespace nxa {
 
-template <int HD>
+// Register budget per (head_dim x row tiles): two waves per SIMD with K/V of two steps in
+// flight up to 128; one wave per SIMD with two steps up to 384; one step beyond that.
+constexpr int decode_waves_per_simd(int hd, int rt) { return hd * rt <= 128 ? 2 : 1; }
+constexpr int decode_depth(int hd, int rt) { return hd * rt <= 384 ? 2 : 1; }
+
+template <int HD, int RT>
 struct DecodeLayout {
     static constexpr int KEYS = kDecodeKeys;                  // 32 keys per wave step
-    static constexpr int CPR = HD / 8;
-    static constexpr int KSTEPS = HD / 16;
-    static constexpr int DBLK = HD / 32;
-    static constexpr int V_ROW = KEYS * 2;                    // bytes per V^T row
-    static constexpr int V_WAVE = HD * V_ROW;                 // per-wave V^T region
-    static constexpr int V_BLOCKS = (KEYS / 4) * CPR;         // (4-key quad, 8-dim chunk) per wave
-    static constexpr int V_LOADS = V_BLOCKS / 64;
-    static constexpr int MERGE_SLOT = (DBLK * 16 * 64 + 2 * 64) * 4;
-    static constexpr int LDS_BYTES = (4 * V_WAVE > 2 * MERGE_SLOT) ? 4 * V_WAVE : 2 * MERGE_SLOT;
-    static_assert(V_LOADS >= 1, "V staging");
+    static constexpr int KS = HD / 32;                        // 32-dim k-steps of S^T
+    static constexpr int DT = HD / 16;                        // 16-dim tiles of O^T
+    static constexpr int VB = (KEYS / 4) * (HD / 8) / 64;     // (4-key, 8-dim) V blocks per lane
+    static constexpr int VT_WAVE = HD * KEYS * 2;             // V^T bytes per wave
+    static constexpr int DEPTH = decode_depth(HD, RT);        // steps of K/V in flight
+    static constexpr int Q_BYTES = RT * KS * 2 * 64 * 16;     // Q^T operands (hi, lo) per workgroup
+    static constexpr int OREGS = RT * DT * 4;                 // f32 O^T values per lane
+    static constexpr int MERGE_SLOT = (OREGS + 2 * RT) * 64 * 4;
+    static constexpr int MAIN_BYTES = (4 * VT_WAVE > 2 * MERGE_SLOT) ? 4 * VT_WAVE : 2 * MERGE_SLOT;
+    static constexpr int LDS_BYTES = MAIN_BYTES + Q_BYTES;
+    static_assert(VB >= 1 && (KEYS / 4) * (HD / 8) % 64 == 0, "V staging");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-__device__ __forceinline__ int dvt_off(int d, int c)
+// V^T byte offset: dim row d (64-byte rows of 32 keys), 8-key chunk c, 4-key half h.  The
+// chunk is XOR-swizzled with bits 1-2 of the row, so the 16 rows an operand read touches
+// (16*dt + 0..15, same chunk) fall on distinct banks within every 8 lanes.
+__device__ __forceinline__ int vt_off(int d, int c, int h)
 {
-    // 64-byte V^T rows; XOR the chunk with (d >> 2) so 16 consecutive rows hit distinct banks.
-    return d * (kDecodeKeys * 2) + 16 * (c ^ ((d >> 2) & 3));
+    return d * (kDecodeKeys * 2) + 16 * (c ^ ((d >> 1) & 3)) + 8 * h;
 }
 
-template <int HD, bool Q_F32, bool O_F32, bool EXT>
-__global__ void __launch_bounds__(kDecodeThreads, HD <= 128 ? 2 : 1)
-decode_kernel(DecodeArgs a)
+constexpr int kAuxNT = 2;   // buffer-load cache policy: non-temporal (streaming K/V)
+
+__device__ __forceinline__ u32x4 buf_load16_nt(rsrc_t r, uint32_t byte_off)
 {
-    using L = DecodeLayout<HD>;
-    constexpr int KSTEPS = L::KSTEPS, DBLK = L::DBLK;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kAuxNT));
+}
+
+template <int HD, int RT, bool Q_F32, bool O_F32, bool EXT>
+__global__ void __launch_bounds__(kDecodeThreads, decode_waves_per_simd(HD, RT))
+decode_part_kernel(DecodeArgs a)
+{
+    using L = DecodeLayout<HD, RT>;
+    constexpr int KS = L::KS, DT = L::DT, VB = L::VB;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n = lane & 31, hh = lane >> 5;
+    const int n = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kvh = blockIdx.y, rg = blockIdx.z;
 
-    // ---- query row of this lane's column: R = draft * G + head-in-group
-    const int R = rg * kDecodeRows + n;
-    const bool row_ok = R < a.n_rows;
-    const int qi = row_ok ? R / a.group : 0;
-    const int h = kvh * a.group + (row_ok ? R - qi * a.group : 0);
-    const int qpos = a.q_base + qi;
-    int row_klo = 0;
-    if (EXT && a.sliding_window > 0 && qpos + 1 > a.sliding_window) row_klo = qpos + 1 - a.sliding_window;
-    const int row_khi = min(qpos, a.n_ctx - 1);
-
-    // ---- Q^T operands (f16 high part + f16 residual for f32 queries)
-    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
-    f16x8 qhi[KSTEPS];
-    f16x8 qlo[Q_F32 ? KSTEPS : 1];
-    {
-        const rsrc_t qr = make_rsrc(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
-        // rows past n_rows point past the descriptor and read as zero
-        const uint32_t qoff = row_ok ? (uint32_t)((((size_t)qi * a.n_q_heads + h) * HD + 8 * hh) * QE) : 0x7fffff00u;
+    // ---- query rows of this lane's columns: R = draft * G + head-in-group
+    int R[RT], qi[RT], h[RT], khi[RT], klo[RT];
+    bool rok[RT];
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            if constexpr (Q_F32) {
-                const f32x4 x0 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks));
-                const f32x4 x1 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks + 16));
-                const f16x8 hi = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
-                qhi[ks] = hi;
-                qlo[ks] = cvt_f16x8(x0[0] - (float)hi[0], x0[1] - (float)hi[1], x0[2] - (float)hi[2],
-                                    x0[3] - (float)hi[3], x1[0] - (float)hi[4], x1[1] - (float)hi[5],
-                                    x1[2] - (float)hi[6], x1[3] - (float)hi[7]);
-            } else {
-                qhi[ks] = as_f16x8(buf_load16(qr, qoff + 32 * ks));
-            }
+    for (int rt = 0; rt < RT; ++rt) {
+        R[rt] = rg * (16 * RT) + 16 * rt + n;
+        rok[rt] = R[rt] < a.n_rows;
+        qi[rt] = rok[rt] ? R[rt] / a.group : 0;
+        h[rt] = kvh * a.group + (rok[rt] ? R[rt] - qi[rt] * a.group : 0);
+        const int qpos = a.q_base + qi[rt];
+        khi[rt] = min(qpos, a.n_ctx - 1);
+        klo[rt] = (EXT && a.sliding_window > 0 && qpos + 1 > a.sliding_window) ? qpos + 1 - a.sliding_window : 0;
+    }
+
+    // ---- Q^T B operands in LDS: lane (row n, group g) holds dims 32*ks + 8*g .. +7, as an
+    // f16 high part and (f32 queries) the f16 residual.  Wave 0 issues the Q loads before
+    // the K/V prologue and converts them once those loads are in flight, so the two
+    // latencies overlap.
+    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
+    constexpr int QV = Q_F32 ? 2 : 1;                           // 16-byte loads per operand
+    uint8_t* qlds = lds + L::MAIN_BYTES;
+    auto qslot = [&](int rt, int ks, int hl) { return qlds + (((rt * KS + ks) * 2 + hl) * 64 + lane) * 16; };
+    u32x4 qraw[RT][KS][QV];
+    if (wave == 0) {
+        const rsrc_t qr = make_rsrc(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            // rows past n_rows point past the descriptor and read as zero
+            const uint32_t qoff = rok[rt] ? (uint32_t)((((size_t)qi[rt] * a.n_q_heads + h[rt]) * HD + 8 * g) * QE)
+                                          : 0x7fffff00u;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int j = 0; j < QV; ++j) qraw[rt][ks][j] = buf_load16(qr, qoff + 32 * QE * ks + 16 * j);
         }
     }
+    auto store_q = [&]() {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                if constexpr (Q_F32) {
+                    const f32x4 x0 = __builtin_bit_cast(f32x4, qraw[rt][ks][0]);
+                    const f32x4 x1 = __builtin_bit_cast(f32x4, qraw[rt][ks][QV - 1]);
+                    const f16x8 hi = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
+                    *(f16x8*)qslot(rt, ks, 0) = hi;
+                    *(f16x8*)qslot(rt, ks, 1) =
+                        cvt_f16x8(x0[0] - (float)hi[0], x0[1] - (float)hi[1], x0[2] - (float)hi[2],
+                                  x0[3] - (float)hi[3], x1[0] - (float)hi[4], x1[1] - (float)hi[5],
+                                  x1[2] - (float)hi[6], x1[3] - (float)hi[7]);
+                } else {
+                    *(f16x8*)qslot(rt, ks, 0) = as_f16x8(qraw[rt][ks][0]);
+                }
+            }
+    };
 
     const int s_begin = a.k_begin + split * a.chunk;
     const int s_end = min(s_begin + a.chunk, a.k_end);
     const int n_sub = s_begin < s_end ? (s_end - s_begin + L::KEYS - 1) / L::KEYS : 0;
+    const int n_my = n_sub > wave ? (n_sub - wave + 3) / 4 : 0;     // steps wave, wave+4, ...
 
     // K/V of this kv head; the descriptors end at this split's last key
     const uint32_t kv_bytes = (uint32_t)max(s_end, 0) * HD * 2;
     const rsrc_t krs = make_rsrc(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     const rsrc_t vrs = make_rsrc(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
-    uint8_t* vw = lds + wave * L::V_WAVE;
+    uint8_t* vw = lds + wave * L::VT_WAVE;
     const float fc = EXT ? 1.f : a.scale_log2;
 
-    f32x16 o[DBLK];
+    // per-lane K rows of the two 16-key tiles: tile t, row n -> key 8*(n/4) + 4t + n%4
+    const uint32_t krow0 = 8 * (n >> 2) + (n & 3);
+    // V^T write bases of this lane (block i adds 4096*i: its dim chunk is 8 further)
+    int vt_wbase[4];
+    {
+        const int kq = lane & 7, cc0 = lane >> 3;
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
-    float m = kNegBig, l = 0.f;
+        for (int k2 = 0; k2 < 4; ++k2) vt_wbase[k2] = 512 * cc0 + 16 * ((kq >> 1) ^ k2) + 8 * (kq & 1);
+    }
 
-    for (int j = wave; j < n_sub; j += 4) {
-        const int key0 = s_begin + L::KEYS * j;
-        // K rows -> A operands: lane (key n, k-group hh)
-        f16x8 ka[KSTEPS];
-        {
-            const uint32_t koff = ((uint32_t)(key0 + n) * HD + 8 * hh) * 2;
+    constexpr int DEPTH = L::DEPTH;
+    u32x4 kb[DEPTH][2 * KS];
+    u32x4 vb[DEPTH][VB][4];
+    auto key0_of = [&](int s) { return s_begin + L::KEYS * (wave + 4 * s); };
+    // K and V of step s into register buffer B (loads past the split read as zero)
+    auto issue = [&](auto B, int s) {
+        constexpr int b = DEPTH == 2 ? decltype(B)::value : 0;
+        const uint32_t key0 = (uint32_t)key0_of(s);
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) ka[ks] = as_f16x8(buf_load16(krs, koff + 32 * ks));
-        }
-        // V rows -> registers: 4 consecutive keys x 8 dims per block
-        u32x4 vr[L::V_LOADS][4];
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int i = 0; i < L::V_LOADS; ++i) {
+            for (int ks = 0; ks < KS; ++ks)
+                kb[b][t * KS + ks] = buf_load16_nt(krs, ((key0 + krow0 + 4 * t) * HD + 32 * ks + 8 * g) * 2);
+#pragma unroll
+        for (int i = 0; i < VB; ++i) {
             const int blk = lane + 64 * i;
             const int kq = blk & 7, cc = blk >> 3;
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4)
-                vr[i][r4] = buf_load16(vrs, ((uint32_t)(key0 + 4 * kq + r4) * HD + 8 * cc) * 2);
+                vb[b][i][r4] = buf_load16_nt(vrs, ((key0 + 4 * kq + r4) * HD + 8 * cc) * 2);
         }
-        // S^T = K Q^T
-        f32x16 s;
+    };
+
+    f32x4 o[RT][DT];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) s[v] = 0.f;
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            s = mfma32x32x16(ka[ks], qhi[ks], s);
-            if constexpr (Q_F32) s = mfma32x32x16(ka[ks], qlo[ks], s);
-        }
-        // V^T -> LDS (keys of each 16-key group in slot order [0-3, 8-11, 4-7, 12-15])
+        for (int dt = 0; dt < DT; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m[RT], l[RT];
 #pragma unroll
-        for (int i = 0; i < L::V_LOADS; ++i) {
-            const int blk = lane + 64 * i;
-            const int kq = blk & 7, cc = blk >> 3;
-            const int q4 = kq & 3;
-            const int pos = ((q4 & 1) << 1) | (q4 >> 1);
-            const int c = 2 * (kq >> 2) + (pos >> 1);
-            const int half = (pos & 1) * 8;
+    for (int rt = 0; rt < RT; ++rt) {
+        m[rt] = kNegBig;
+        l[rt] = 0.f;
+    }
+
+    // step s consumes register buffer B = s & 1 (buffer 0 at depth 1), then refills it with
+    // step s + DEPTH
+    auto step = [&](auto B, int s) {
+        constexpr int b = DEPTH == 2 ? decltype(B)::value : 0;
+        const int key0 = key0_of(s);
+        // S^T = K Q^T for the two 16-key tiles
+        f32x4 sc[2][RT];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) sc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const f16x8 qh = *(const f16x8*)qslot(rt, ks, 0);
+                f16x8 ql;
+                if constexpr (Q_F32) ql = *(const f16x8*)qslot(rt, ks, 1);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const f16x8 ka = as_f16x8(kb[b][t * KS + ks]);
+                    sc[t][rt] = mfma16x16x32(ka, qh, sc[t][rt]);
+                    if constexpr (Q_F32) sc[t][rt] = mfma16x16x32(ka, ql, sc[t][rt]);
+                }
+            }
+        // V^T of this step -> LDS: block (key quad kq, dim chunk cc) becomes 8 rows of 4 keys.
+        // Row 8*cc + dd, chunk kq/2 lands at vt_off = 512*cc + 64*dd + 16*((kq/2) ^ (dd/2)) +
+        // 8*(kq%2): four lane-dependent bases (one per dd/2) plus immediates.
+#pragma unroll
+        for (int i = 0; i < VB; ++i) {
 #pragma unroll
             for (int dd = 0; dd < 8; ++dd) {
-                const int d = 8 * cc + dd;
                 const int wj = dd >> 1;
                 const uint32_t sel = (dd & 1) ? kSelHi : kSelLo;
                 u32x2 val;
-                val[0] = perm_b32(vr[i][1][wj], vr[i][0][wj], sel);
-                val[1] = perm_b32(vr[i][3][wj], vr[i][2][wj], sel);
-                *(u32x2*)(vw + dvt_off(d, c) + half) = val;
+                val[0] = perm_b32(vb[b][i][1][wj], vb[b][i][0][wj], sel);
+                val[1] = perm_b32(vb[b][i][3][wj], vb[b][i][2][wj], sel);
+                *(u32x2*)(vw + vt_wbase[dd >> 1] + 4096 * i + 64 * dd) = val;
             }
         }
+        // both register halves of this step are consumed: refill them with step s + DEPTH.  The
+        // loads are unconditional (steps past the split read as zero through the descriptor
+        // and touch no memory), so every iteration issues the same loads in the same order
+        // and the compiler's wait counts keep two steps in flight.
+        __builtin_amdgcn_sched_barrier(0);
+        issue(B, s + DEPTH);
+        __builtin_amdgcn_sched_barrier(0);
         wave_lds_sync();
-        // mask, softmax update
-        float mx = -INFINITY;
+        // mask, online softmax (log2 units)
+        f16x8 pb[RT];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = key0 + 8 * (v >> 2) + 4 * hh + (v & 3);
-            float x = s[v];
-            if constexpr (EXT) {
-                x *= a.scale;
-                if (a.softcap > 0.f) x = a.softcap * tanhf(x / a.softcap);
-                x *= kLog2e;
+        for (int rt = 0; rt < RT; ++rt) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = key0 + 8 * g + 4 * t + i;
+                    float x = sc[t][rt][i];
+                    if constexpr (EXT) {
+                        x *= a.scale;
+                        if (a.softcap > 0.f) x = a.softcap * tanhf(x / a.softcap);
+                        x *= kLog2e;
+                    }
+                    const bool vis = rok[rt] && key < s_end && key <= khi[rt] && key >= klo[rt];
+                    x = vis ? x : -INFINITY;
+                    sc[t][rt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m[rt], mx * fc);
+            if (__any(m_new != m[rt])) {
+                const float corr = fast_exp2(m[rt] - m_new);
+                l[rt] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[rt][dt] *= corr;
+                m[rt] = m_new;
             }
-            const bool vis = row_ok && key < s_end && key <= row_khi && key >= row_klo;
-            if (!vis) x = -INFINITY;
-            s[v] = x;
-            mx = fmaxf(mx, x);
+            float p[8];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[4 * t + i] = fast_exp2(fmaf(sc[t][rt][i], fc, -m[rt]));
+            l[rt] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            pb[rt] = cvt_f16x8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
         }
-        mx = fmaxf(mx, xor32(mx));
-        const float m_new = fmaxf(m, mx * fc);
-        const float corr = fast_exp2(m - m_new);
-        float p[16];
-        float lsum = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            p[v] = fast_exp2(fmaf(s[v], fc, -m_new));
-            lsum += p[v];
-        }
-        l = l * corr + lsum;
-        m = m_new;
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[db][v] *= corr;
-        const f16x8 pb0 = cvt_f16x8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
-        const f16x8 pb1 = cvt_f16x8(p[8], p[9], p[10], p[11], p[12], p[13], p[14], p[15]);
         // O^T += V^T P^T
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db) {
-            const int d = 32 * db + n;
-            const f16x8 va0 = *(const f16x8*)(vw + dvt_off(d, hh));
-            const f16x8 va1 = *(const f16x8*)(vw + dvt_off(d, 2 + hh));
-            o[db] = mfma32x32x16(va0, pb0, o[db]);
-            o[db] = mfma32x32x16(va1, pb1, o[db]);
+        for (int dt = 0; dt < DT; ++dt) {
+            const f16x8 va = *(const f16x8*)(vw + vt_off(16 * dt + n, g, 0));
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) o[rt][dt] = mfma16x16x32(va, pb[rt], o[rt][dt]);
         }
         wave_lds_sync();
+    };
+
+    // Steps run in pairs (static buffer indices); an odd count gets one fully masked step.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // The prologue issues in the same order as the loop (K then V, step by step), so the
+    // wait counts at the loop header stay those of the steady state.
+    __builtin_amdgcn_sched_barrier(0);
+    issue(I0{}, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DEPTH == 2) issue(I1{}, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave == 0) store_q();
+    __syncthreads();
+    for (int s = 0; s < n_my; s += 2) {
+        step(I0{}, s);
+        step(I1{}, s + 1);
     }
 
-    // ---- merge the 4 waves' (m, l, O) in LDS (log2 units)
-    float l_tot = l + xor32(l);
+    // ---- row sums across the four lanes of a row, then merge the 4 waves in LDS
+    float lt[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        lt[rt] = l[rt] + __shfl_xor(l[rt], 16);
+        lt[rt] += __shfl_xor(lt[rt], 32);
+    }
     __syncthreads();                                       // V^T regions are reused below
     float* slot0 = (float*)lds;
     float* slot1 = (float*)(lds + L::MERGE_SLOT);
     auto put = [&](float* sl) {
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db)
+        for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) sl[(db * 16 + v) * 64 + lane] = o[db][v];
-        sl[DBLK * 16 * 64 + lane] = m;
-        sl[DBLK * 16 * 64 + 64 + lane] = l_tot;
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sl[((rt * DT + dt) * 4 + i) * 64 + lane] = o[rt][dt][i];
+            sl[(L::OREGS + 2 * rt) * 64 + lane] = m[rt];
+            sl[(L::OREGS + 2 * rt + 1) * 64 + lane] = lt[rt];
+        }
     };
     auto take = [&](const float* sl) {
-        const float m2 = sl[DBLK * 16 * 64 + lane];
-        const float l2 = sl[DBLK * 16 * 64 + 64 + lane];
-        const float M = fmaxf(m, m2);
-        const float c1 = fast_exp2(m - M), c2 = fast_exp2(m2 - M);
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db)
+        for (int rt = 0; rt < RT; ++rt) {
+            const float m2 = sl[(L::OREGS + 2 * rt) * 64 + lane];
+            const float l2 = sl[(L::OREGS + 2 * rt + 1) * 64 + lane];
+            const float M = fmaxf(m[rt], m2);
+            const float c1 = fast_exp2(m[rt] - M), c2 = fast_exp2(m2 - M);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[db][v] = o[db][v] * c1 + sl[(db * 16 + v) * 64 + lane] * c2;
-        l_tot = l_tot * c1 + l2 * c2;
-        m = M;
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[rt][dt][i] = o[rt][dt][i] * c1 + sl[((rt * DT + dt) * 4 + i) * 64 + lane] * c2;
+            lt[rt] = lt[rt] * c1 + l2 * c2;
+            m[rt] = M;
+        }
     };
-    auto merge_waves = [&]() {                             // result in wave 0
-        if (wave >= 2) put(wave == 2 ? slot0 : slot1);
-        __syncthreads();
-        if (wave < 2) take(wave == 0 ? slot0 : slot1);
-        __syncthreads();
-        if (wave == 1) put(slot0);
-        __syncthreads();
-        if (wave == 0) take(slot0);
-    };
-    auto store_out = [&]() {                               // wave 0: normalised output row
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        const size_t obase = ((size_t)qi * a.n_q_heads + h) * HD;
+    if (wave >= 2) put(wave == 2 ? slot0 : slot1);
+    __syncthreads();
+    if (wave < 2) take(wave == 0 ? slot0 : slot1);
+    __syncthreads();
+    if (wave == 1) put(slot0);
+    __syncthreads();
+    if (wave != 0) return;
+    take(slot0);
+
+    // ---- wave 0: lane (row n, group g) holds dims 16*dt + 4*g + (0..3) of its rows
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db)
+    for (int rt = 0; rt < RT; ++rt) {
+        if (!rok[rt]) continue;
+        const size_t prow = (size_t)qi[rt] * a.n_q_heads + h[rt];
+        if (a.n_splits == 1) {
+            const float inv = lt[rt] > 0.f ? 1.f / lt[rt] : 0.f;
 #pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                const int dim = 32 * db + 8 * a4 + 4 * hh;
-                const float v0 = o[db][4 * a4] * inv, v1 = o[db][4 * a4 + 1] * inv;
-                const float v2 = o[db][4 * a4 + 2] * inv, v3 = o[db][4 * a4 + 3] * inv;
+            for (int dt = 0; dt < DT; ++dt) {
+                const int dim = 16 * dt + 4 * g;
+                const f32x4 y = o[rt][dt] * inv;
                 if constexpr (O_F32) {
-                    f32x4 x = {v0, v1, v2, v3};
-                    *(f32x4*)((float*)a.out + obase + dim) = x;
+                    *(f32x4*)((float*)a.out + prow * HD + dim) = y;
                 } else {
-                    f32x2 p0 = {v0, v1}, p1 = {v2, v3};
+                    f32x2 p0 = {y[0], y[1]}, p1 = {y[2], y[3]};
                     f16x2 h0 = __builtin_convertvector(p0, f16x2);
                     f16x2 h1 = __builtin_convertvector(p1, f16x2);
                     u32x2 x = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
-                    *(u32x2*)((uint16_t*)a.out + obase + dim) = x;
+                    *(u32x2*)((uint16_t*)a.out + prow * HD + dim) = x;
                 }
             }
-    };
-    merge_waves();
-    if (a.n_splits == 1) {
-        if (wave == 0 && row_ok) store_out();
-        return;
-    }
-
-    // ---- publish this split's partial; the last split to arrive merges all of them
-    const size_t prow = (size_t)qi * a.n_q_heads + h;
-    if (wave == 0 && row_ok) {
-        float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
+        } else {
+            float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                const int dim = 32 * db + 8 * a4 + 4 * hh;
-                f32x2 x0 = {o[db][4 * a4], o[db][4 * a4 + 1]};
-                f32x2 x1 = {o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
-                *(f32x2*)(pr + dim) = x0;
-                *(f32x2*)(pr + dim + 2) = x1;
+            for (int dt = 0; dt < DT; ++dt) {
+                const int dim = 16 * dt + 4 * g;
+                *(f32x2*)(pr + dim) = f32x2{o[rt][dt][0], o[rt][dt][1]};
+                *(f32x2*)(pr + dim + 2) = f32x2{o[rt][dt][2], o[rt][dt][3]};
             }
-        if (hh == 0) {
-            pr[HD] = m * kLn2;               // natural-log units, as qwen35_attn_part.comp stores m
-            pr[HD + 1] = l_tot;
+            if (g == 0) *(f32x2*)(pr + HD) = f32x2{m[rt] * kLn2, lt[rt]};   // m in natural-log units
         }
     }
-    release_agent();
-    __shared__ int s_last;
-    __syncthreads();
-    if (!a.fused_merge) return;                            // a combine kernel follows
-    unsigned int* cnt = a.counters + (size_t)kvh * gridDim.z + rg;
-    if (tid == 0) s_last = arrive_is_last(cnt, (unsigned int)a.n_splits);
-    __syncthreads();
-    if (!s_last) return;
-    acquire_agent();
-    // wave w folds splits w, w + 4, ... of its rows, then the 4 waves merge in LDS
-    m = kNegBig;
-    l_tot = 0.f;
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
-    if (row_ok) {
-        for (int s2 = wave; s2 < a.n_splits; s2 += 4) {
-            const float* pr = a.part + (prow * a.n_splits + s2) * (HD + 2);
-            const float m2 = pr[HD] * kLog2e, l2 = pr[HD + 1];
-            const float M = fmaxf(m, m2);
-            const float c1 = fast_exp2(m - M), c2 = fast_exp2(m2 - M);
-#pragma unroll
-            for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    const int dim = 32 * db + 8 * a4 + 4 * hh;
-                    const f32x2 x0 = *(const f32x2*)(pr + dim);
-                    const f32x2 x1 = *(const f32x2*)(pr + dim + 2);
-                    o[db][4 * a4] = o[db][4 * a4] * c1 + x0[0] * c2;
-                    o[db][4 * a4 + 1] = o[db][4 * a4 + 1] * c1 + x0[1] * c2;
-                    o[db][4 * a4 + 2] = o[db][4 * a4 + 2] * c1 + x1[0] * c2;
-                    o[db][4 * a4 + 3] = o[db][4 * a4 + 3] * c1 + x1[1] * c2;
-                }
-            l_tot = l_tot * c1 + l2 * c2;
-            m = M;
-        }
-    }
-    __syncthreads();
-    merge_waves();
-    if (wave == 0 && row_ok) store_out();
-    if (tid == 0) counter_reset(cnt);
 }
 
-// ---- LSE combine for large fan-in (qwen35_attn_comb.comp:16-40 without the gate):
+// ---- LSE combine (qwen35_attn_comb.comp:16-40 without the gate):
 // out[row][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, zeros for a row that
-// saw no key.  One wave per (row, 64-dim chunk); split weights are computed once per wave.
-constexpr int kCombineThreads = 64;
+// saw no key.  One workgroup per row: thread (split group sg, dim pair dp) folds splits
+// sg, sg + G, ... of dims 2dp, 2dp+1.  All of a thread's loads (its acc pairs and the
+// (m, l) pair every lane of a wave shares) are independent, so a batch of 16 splits is one
+// memory round trip; the G groups then merge through LDS.
+template <int HD>
+struct CombineLayout {
+    static constexpr int DP = HD / 2;                          // dim pairs per row
+    static constexpr int G = DP >= 256 ? 1 : 256 / DP;         // split groups
+    static constexpr int THREADS = DP * G;
+    static constexpr int BATCH = 16;                           // splits in flight per thread
+};
 
 template <int HD, bool O_F32>
-__global__ void __launch_bounds__(kCombineThreads)
+__global__ void __launch_bounds__(CombineLayout<HD>::THREADS)
 combine_kernel(CombineArgs a)
 {
-    __shared__ float wgt[kMaxSplits];
-    const int row = blockIdx.x, lane = threadIdx.x;
-    const int d = blockIdx.y * kCombineThreads + lane;
+    using C = CombineLayout<HD>;
+    __shared__ float sm_m[C::G], sm_l[C::G];
+    __shared__ f32x2 sm_acc[C::G][C::DP];
+    const int row = blockIdx.x;
+    const int dp = threadIdx.x % C::DP, sg = threadIdx.x / C::DP;
     const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
-    float mx = -3.0e38f;
-    for (int c = lane; c < a.n_splits; c += kCombineThreads) mx = fmaxf(mx, pr[(size_t)c * (HD + 2) + HD]);
+
+    float M = kNegBig * 4.f, L = 0.f;               // below any partial's m (kNegBig)
+    f32x2 acc = {0.f, 0.f};
+    for (int c0 = sg; c0 < a.n_splits; c0 += C::G * C::BATCH) {
+        f32x2 x[C::BATCH], ml[C::BATCH];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    float lsum = 0.f;
-    for (int c = lane; c < a.n_splits; c += kCombineThreads) {
-        const float w = fast_exp2((pr[(size_t)c * (HD + 2) + HD] - mx) * kLog2e);
-        wgt[c] = w;
-        lsum += w * pr[(size_t)c * (HD + 2) + HD + 1];
+        for (int j = 0; j < C::BATCH; ++j) {
+            const int c = c0 + j * C::G;
+            const bool ok = c < a.n_splits;
+            const float* ps = pr + (size_t)(ok ? c : 0) * (HD + 2);
+            x[j] = *(const f32x2*)(ps + 2 * dp);
+            ml[j] = *(const f32x2*)(ps + HD);
+            if (!ok) {
+                x[j] = f32x2{0.f, 0.f};
+                ml[j] = f32x2{kNegBig * 4.f, 0.f};
+            }
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < C::BATCH; ++j) Mb = fmaxf(Mb, ml[j][0]);
+        const float cr = fast_exp2((M - Mb) * kLog2e);
+        acc *= cr;
+        L *= cr;
+#pragma unroll
+        for (int j = 0; j < C::BATCH; ++j) {
+            const float w = fast_exp2((ml[j][0] - Mb) * kLog2e);
+            acc += x[j] * w;
+            L += ml[j][1] * w;
+        }
+        M = Mb;
     }
+    if constexpr (C::G > 1) {
+        if (dp == 0) {
+            sm_m[sg] = M;
+            sm_l[sg] = L;
+        }
+        sm_acc[sg][dp] = acc;
+        __syncthreads();
+        if (sg != 0) return;
+        float Mt = sm_m[0];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
-    __syncthreads();
-    if (d >= HD) return;
-    float acc = 0.f;
-    for (int c = 0; c < a.n_splits; ++c) acc += pr[(size_t)c * (HD + 2) + d] * wgt[c];
-    const float y = lsum > 0.f ? acc / lsum : 0.f;
-    if constexpr (O_F32) ((float*)a.out)[(size_t)row * HD + d] = y;
-    else ((_Float16*)a.out)[(size_t)row * HD + d] = (_Float16)y;
+        for (int j = 1; j < C::G; ++j) Mt = fmaxf(Mt, sm_m[j]);
+        acc = f32x2{0.f, 0.f};
+        L = 0.f;
+#pragma unroll
+        for (int j = 0; j < C::G; ++j) {
+            const float w = fast_exp2((sm_m[j] - Mt) * kLog2e);
+            acc += sm_acc[j][dp] * w;
+            L += sm_l[j] * w;
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const f32x2 y = acc * inv;
+    if constexpr (O_F32) {
+        *(f32x2*)((float*)a.out + (size_t)row * HD + 2 * dp) = y;
+    } else {
+        const f16x2 hy = __builtin_convertvector(y, f16x2);
+        *(f16x2*)((_Float16*)a.out + (size_t)row * HD + 2 * dp) = hy;
+    }
 }
 
 template <int HD, bool OF>
 static hipError_t launch_combine_t(const CombineArgs& a, hipStream_t stream)
 {
-    hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows, (HD + kCombineThreads - 1) / kCombineThreads),
-                       dim3(kCombineThreads), 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows), dim3(CombineLayout<HD>::THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -386,38 +499,48 @@ hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStr
     }
 }
 
-template <int HD, bool QF, bool OF, bool EXT>
+template <int HD, int RT, bool QF, bool OF, bool EXT>
 static hipError_t launch_decode_t(const DecodeArgs& a, int n_rowgroups, hipStream_t stream)
 {
-    constexpr int lds_bytes = DecodeLayout<HD>::LDS_BYTES;
+    constexpr int lds_bytes = DecodeLayout<HD, RT>::LDS_BYTES;
     static bool attr_done = false;        // set once per instantiation (idempotent)
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)decode_kernel<HD, QF, OF, EXT>,
+        hipError_t e = hipFuncSetAttribute((const void*)decode_part_kernel<HD, RT, QF, OF, EXT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    hipLaunchKernelGGL((decode_kernel<HD, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
+    hipLaunchKernelGGL((decode_part_kernel<HD, RT, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
                        dim3(kDecodeThreads), lds_bytes, stream, a);
     return hipGetLastError();
 }
 
-template <int HD, bool QF>
-static hipError_t launch_decode_q(const DecodeArgs& a, bool o_f32, bool ext, int nrg, hipStream_t s)
+template <int HD, int RT>
+static hipError_t launch_decode_rt(const DecodeArgs& a, bool q_f32, bool o_f32, bool ext, int nrg, hipStream_t s)
 {
-    if (ext) return o_f32 ? launch_decode_t<HD, QF, true, true>(a, nrg, s) : launch_decode_t<HD, QF, false, true>(a, nrg, s);
-    return o_f32 ? launch_decode_t<HD, QF, true, false>(a, nrg, s) : launch_decode_t<HD, QF, false, false>(a, nrg, s);
+    if (ext) {
+        if (q_f32) return o_f32 ? launch_decode_t<HD, RT, true, true, true>(a, nrg, s)
+                                : launch_decode_t<HD, RT, true, false, true>(a, nrg, s);
+        return o_f32 ? launch_decode_t<HD, RT, false, true, true>(a, nrg, s)
+                     : launch_decode_t<HD, RT, false, false, true>(a, nrg, s);
+    }
+    if (q_f32) return o_f32 ? launch_decode_t<HD, RT, true, true, false>(a, nrg, s)
+                            : launch_decode_t<HD, RT, true, false, false>(a, nrg, s);
+    return o_f32 ? launch_decode_t<HD, RT, false, true, false>(a, nrg, s)
+                 : launch_decode_t<HD, RT, false, false, false>(a, nrg, s);
 }
 
 template <int HD>
 static hipError_t launch_decode_hd(const DecodeArgs& a, bool q_f32, bool o_f32, bool ext, int nrg, hipStream_t s)
 {
-    return q_f32 ? launch_decode_q<HD, true>(a, o_f32, ext, nrg, s) : launch_decode_q<HD, false>(a, o_f32, ext, nrg, s);
+    return a.row_tiles == 1 ? launch_decode_rt<HD, 1>(a, q_f32, o_f32, ext, nrg, s)
+                            : launch_decode_rt<HD, 2>(a, q_f32, o_f32, ext, nrg, s);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream)
 {
+    if (a.row_tiles != 1 && a.row_tiles != 2) return hipErrorInvalidValue;
     switch (head_dim) {
     case 64: return launch_decode_hd<64>(a, q_f32, o_f32, ext, n_rowgroups, stream);
     case 128: return launch_decode_hd<128>(a, q_f32, o_f32, ext, n_rowgroups, stream);

@@ -23,8 +23,8 @@
 //    the last query), so rows past it read as zero with no branch in the loop.
 //  * Optional split of the key range over n_splits workgroups (short chunks over a long
 //    cache, e.g. 512 queries after 4096 cached tokens).  Each split writes fp32 partials
-//    (acc, m, l); the last workgroup of a (query block, head) to arrive merges them with
-//    the LSE rule of qwen35_attn_comb.comp:16-40 and writes the output -- no second pass.
+//    (acc, m, l) in the reference's split-K format; the decode path's combine kernel merges
+//    them with the LSE rule of qwen35_attn_comb.comp:16-40.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -318,7 +318,7 @@ prefill_kernel(PrefillArgs a)
         return;
     }
 
-    // ---- split-KV: publish this split's partial, the last arriver merges all of them
+    // ---- split-KV: publish this split's partial; the combine kernel merges the splits
     const size_t prow = (size_t)qrow * a.n_q_heads + h;
     if (row_ok) {
         float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
@@ -327,55 +327,11 @@ prefill_kernel(PrefillArgs a)
 #pragma unroll
             for (int a4 = 0; a4 < 4; ++a4) {
                 const int dim = 32 * db + 8 * a4 + 4 * hh;
-                f32x2 x0 = {o[db][4 * a4], o[db][4 * a4 + 1]};
-                f32x2 x1 = {o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
-                *(f32x2*)(pr + dim) = x0;
-                *(f32x2*)(pr + dim + 2) = x1;
+                *(f32x2*)(pr + dim) = f32x2{o[db][4 * a4], o[db][4 * a4 + 1]};
+                *(f32x2*)(pr + dim + 2) = f32x2{o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
             }
-        if (hh == 0) {
-            pr[HD] = m_used * kLn2;          // natural-log units
-            pr[HD + 1] = l_tot;
-        }
+        if (hh == 0) *(f32x2*)(pr + HD) = f32x2{m_used * kLn2, l_tot};   // m in natural-log units
     }
-    release_agent();
-    __shared__ int s_last;
-    __syncthreads();
-    unsigned int* cnt = a.counters + (size_t)qb * a.n_q_heads + h;
-    if (tid == 0) s_last = arrive_is_last(cnt, (unsigned int)a.n_splits);
-    __syncthreads();
-    if (!s_last) return;
-    acquire_agent();
-    if (row_ok) {
-        // fold splits 0..n-1 in index order, so the result does not depend on arrival order
-        float m_nat = kNegBig;
-        l_tot = 0.f;
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
-        for (int s2 = 0; s2 < a.n_splits; ++s2) {
-            const float* pr = a.part + (prow * a.n_splits + s2) * (HD + 2);
-            const float m2 = pr[HD], l2 = pr[HD + 1];
-            const float M = fmaxf(m_nat, m2);
-            const float c1 = fast_exp2((m_nat - M) * kLog2e), c2 = fast_exp2((m2 - M) * kLog2e);
-#pragma unroll
-            for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    const int dim = 32 * db + 8 * a4 + 4 * hh;
-                    const f32x2 x0 = *(const f32x2*)(pr + dim);
-                    const f32x2 x1 = *(const f32x2*)(pr + dim + 2);
-                    o[db][4 * a4] = o[db][4 * a4] * c1 + x0[0] * c2;
-                    o[db][4 * a4 + 1] = o[db][4 * a4 + 1] * c1 + x0[1] * c2;
-                    o[db][4 * a4 + 2] = o[db][4 * a4 + 2] * c1 + x1[0] * c2;
-                    o[db][4 * a4 + 3] = o[db][4 * a4 + 3] * c1 + x1[1] * c2;
-                }
-            l_tot = l_tot * c1 + l2 * c2;
-            m_nat = M;
-        }
-        store_out(l_tot > 0.f ? 1.f / l_tot : 0.f);
-    }
-    if (tid == 0) counter_reset(cnt);
 }
 
 // ---- launchers

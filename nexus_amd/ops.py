@@ -65,7 +65,7 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_head
         need = capi.prefill_ws_bytes(desc)
         if need > 0:
             if workspace is None or workspace.numel() * workspace.element_size() < need:
-                workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+                workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
             ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(q.device).cuda_stream
     capi.prefill_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws_ptr,
@@ -88,7 +88,7 @@ def attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads
     if need <= 0:
         raise capi.NexusAttnError(capi.NEXUS_E_UNSUPPORTED, capi.last_error() or "bad shape")
     if partial_ws is None or partial_ws.numel() * partial_ws.element_size() < need:
-        partial_ws = torch.zeros(need // 4, dtype=torch.float32, device=q.device)
+        partial_ws = torch.empty(need // 4, dtype=torch.float32, device=q.device)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     capi.decode_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                     partial_ws.data_ptr(), n_splits, stream)

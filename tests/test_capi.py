@@ -100,14 +100,10 @@ def test_null_pointers_declined():
 
 
 def test_workspace_sizes():
-    # decode: f32 partials [n_query*Hq][n_splits][hd+2], then one 8-byte counter per
-    # (kv head, row group), 256-byte aligned
-    def align(x):
-        return (x + 255) // 256 * 256
-
+    # decode: f32 partials [n_query*Hq][n_splits][hd+2] and nothing else (no state)
     d = capi.make_desc(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=1, q_base_pos=61439, n_ctx=61440)
-    assert capi.decode_ws_bytes(d, 64) == align(40 * 64 * 130 * 4) + 8 * 8
-    assert capi.decode_ws_bytes(d, 0) == align(40 * capi.decode_default_splits(d) * 130 * 4) + 8 * 8
+    assert capi.decode_ws_bytes(d, 64) == 40 * 64 * 130 * 4
+    assert capi.decode_ws_bytes(d, 0) == 40 * capi.decode_default_splits(d) * 130 * 4
     assert capi.decode_ws_bytes(_desc(head_dim=96), 4) == 0
     # a cold 8192 prompt with 40 heads fills the GPU unsplit: no workspace
     cold = capi.make_desc(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=8192, q_base_pos=0, n_ctx=8192)

@@ -176,32 +176,31 @@ def test_decode_partials_have_reference_meaning(hip):
 
 
 def test_repeated_calls_reuse_workspace(hip):
-    """The arrival counters are left at zero: repeated calls on one workspace agree bit for
-    bit, for the fused merge (decode, prefill split) and the combine-kernel path."""
+    """The workspace carries no state between calls: a workspace full of NaN garbage, and
+    repeated calls on one workspace, give bit-identical outputs (decode with and without
+    row tiles, prefill split path)."""
     import torch
 
     cases = [("decode", 40, 8, 128, 1, 3000, 16), ("decode", 16, 2, 256, 4, 3000, 200),
              ("prefill", 8, 2, 128, 200, 2500, 0)]
     for kind, hq, hkv, hd, nq, base, splits in cases:
+        print(f"[case] workspace reuse {kind} hq={hq} hkv={hkv} hd={hd} nq={nq}", flush=True)
         q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=9)
         qt, kt, vt = dev(q), dev(k), dev(v)
         if kind == "decode":
             d = capi.make_desc(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, q_base_pos=base, n_ctx=base + nq)
-            ws = torch.zeros(capi.decode_ws_bytes(d, splits) // 4, dtype=torch.float32, device="cuda")
+            ws = torch.full((capi.decode_ws_bytes(d, splits) // 4,), float("nan"), dtype=torch.float32, device="cuda")
             outs = [ops.attn_decode(qt, kt, vt, n_kv_heads=hkv, q_base_pos=base, n_ctx=base + nq,
                                     n_splits=splits, partial_ws=ws).cpu().numpy() for _ in range(3)]
         else:
             qt = qt.half()
             d = ops.make_desc_for(qt, kt, n_kv_heads=hkv, q_base_pos=base, n_ctx=base + nq)
-            ws = torch.zeros(max(capi.prefill_ws_bytes(d), 256), dtype=torch.uint8, device="cuda")
+            ws = torch.full((max(capi.prefill_ws_bytes(d), 256) // 4,), float("nan"), dtype=torch.float32,
+                            device="cuda")
             outs = [ops.attn_prefill(qt, kt, vt, n_kv_heads=hkv, q_base_pos=base, n_ctx=base + nq,
                                      workspace=ws).float().cpu().numpy() for _ in range(3)]
+        assert np.all(np.isfinite(outs[0])), kind
         assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2]), kind
-        nrow = nq * hq
-        cnt_off = (nrow * max(splits, 1) * (hd + 2) * 4 + 255) // 256 * 256
-        if kind == "decode":
-            counters = ws.view(torch.uint8)[cnt_off:].cpu().numpy()
-            assert not counters.any(), "arrival counters not reset"
 
 
 def test_decode_split_count_invariance(hip):
