@@ -31,6 +31,9 @@ COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     # packed FP32 (v_pk_*_f32) stays off in every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no NaN semantics are relied on (masking uses infinities): max/min need no input
+    # canonicalisation
+    "-fno-honor-nans",
     "-Wall",
     "-Wno-unused-function",
     f"-I{ROOT / 'include'}",

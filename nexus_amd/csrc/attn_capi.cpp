@@ -165,18 +165,21 @@ size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
     return nxa::ws_partial_bytes((long long)d->n_query * d->n_q_heads, splits, d->head_dim);
 }
 
-// Split count of the prefill kernel: enough (query block, head, split) workgroups to fill
-// two per CU (one for head_dim 256), each split keeping >= 4 key tiles.
+// Split count of the prefill kernel.  Splitting costs a partial write + read per row and
+// split plus a combine launch, which only pays off when the unsplit grid leaves most CUs
+// idle (measured on MI355X: 160 workgroups of 512 queries x 40 heads run faster unsplit
+// than in 3 splits).  Below half a workgroup per CU, split so the grid reaches about one
+// workgroup per CU, each split keeping >= 4 key tiles.
 int prefill_splits(const nexus_attn_desc* d)
 {
     const long long qblocks = (d->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
     const long long base = qblocks * d->n_q_heads;
-    const long long target = (long long)(d->head_dim <= 128 ? 2 : 1) * device_cus();
-    if (base >= target) return 1;
-    long long s = target / base;
+    const long long cus = device_cus();
+    if (2 * base >= cus) return 1;
+    long long s = cus / base;
     int kb, ke;
     key_range(d, &kb, &ke);
-    const long long tiles = (ke - kb + nxa::kPrefillBN - 1) / nxa::kPrefillBN;
+    const long long tiles = (ke - kb + 63) / 64;
     if (s > tiles / 4) s = tiles / 4;
     if (s > 16) s = 16;
     return s < 1 ? 1 : (int)s;

@@ -64,6 +64,45 @@ __device__ __forceinline__ f16x8 cvt_f16x8(float a0, float a1, float a2, float a
 // Value of the same register in lane (l ^ 32): pairs the two k-groups of a 32x32 tile.
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 
+// Cross-lane reductions on the VALU (v_permlane{16,32}_swap, no LDS round trip).  The
+// instruction swaps the upper half (lanes 32-63, or the odd 16-lane rows) of its first
+// operand with the lower half (lanes 0-31, or the even rows) of its second; with both
+// starting as x, the pair then holds x[l] and x[l ^ 32] (or x[l ^ 16]) in every lane, so
+// max/sum of the pair is the reduction over the two lanes.  Issued as inline asm so the two
+// results are two registers (s_nop 1: two wait states after the VALU writes of x).
+__device__ __forceinline__ void swap_halves32(float& a, float& b)
+{
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows16(float& a, float& b)
+{
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float max_xor32(float x)
+{
+    float a = x, b = x;
+    swap_halves32(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor32(float x)
+{
+    float a = x, b = x;
+    swap_halves32(a, b);
+    return a + b;
+}
+__device__ __forceinline__ float max_xor16(float x)
+{
+    float a = x, b = x;
+    swap_rows16(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor16(float x)
+{
+    float a = x, b = x;
+    swap_rows16(a, b);
+    return a + b;
+}
+
 // Byte permute of two dwords (v_perm_b32): selector bytes 0-3 pick from lo, 4-7 from hi.
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel)
 {
@@ -101,6 +140,16 @@ constexpr int kRsrcWord3 = 0x00020000;     // raw 32-bit dword buffer, gfx9 fami
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+// Same, for a base and size that are uniform across the wave: readfirstlane keeps the
+// descriptor in scalar registers (a descriptor the compiler places in vector registers
+// turns every buffer access into a waterfall loop).
+__device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, uint32_t bytes)
+{
+    const uint64_t p = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    return make_rsrc((const void*)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
 }
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t byte_off)
 {

@@ -25,7 +25,7 @@
 //  * The 32 keys of a step form two 16-key S^T tiles whose rows are the keys
 //    8*(r/4) + 4*t + (r%4) (tile t, row r).  The D layout then leaves lane (row n, group g)
 //    holding keys 8g..8g+7 of row n -- exactly the B operand of O^T += V^T P^T, so P
-//    needs no shuffle.  Row max/sum: two cross-lane exchanges (lane ^ 16, lane ^ 32).
+//    needs no shuffle.  Row max/sum: v_permlane16_swap + v_permlane32_swap on the VALU.
 //  * V rows are transposed into a wave-private LDS region (v_perm, 8-byte writes) and read
 //    back as V^T A operands (16 bytes = 8 keys of one dim).
 //  * Software pipeline over register double buffers: K and V of step s + 2 are issued as
@@ -84,7 +84,9 @@ decode_part_kernel(DecodeArgs a)
     constexpr int KS = L::KS, DT = L::DT, VB = L::VB;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index is uniform across the wave: readfirstlane lets the compiler keep
+    // per-wave bounds and branches scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kvh = blockIdx.y, rg = blockIdx.z;
 
@@ -112,7 +114,7 @@ decode_part_kernel(DecodeArgs a)
     auto qslot = [&](int rt, int ks, int hl) { return qlds + (((rt * KS + ks) * 2 + hl) * 64 + lane) * 16; };
     u32x4 qraw[RT][KS][QV];
     if (wave == 0) {
-        const rsrc_t qr = make_rsrc(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
+        const rsrc_t qr = make_rsrc_uniform(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             // rows past n_rows point past the descriptor and read as zero
@@ -151,8 +153,8 @@ decode_part_kernel(DecodeArgs a)
 
     // K/V of this kv head; the descriptors end at this split's last key
     const uint32_t kv_bytes = (uint32_t)max(s_end, 0) * HD * 2;
-    const rsrc_t krs = make_rsrc(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
-    const rsrc_t vrs = make_rsrc(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    const rsrc_t krs = make_rsrc_uniform(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    const rsrc_t vrs = make_rsrc_uniform(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     uint8_t* vw = lds + wave * L::VT_WAVE;
     const float fc = EXT ? 1.f : a.scale_log2;
 
@@ -270,8 +272,7 @@ decode_part_kernel(DecodeArgs a)
                     sc[t][rt][i] = x;
                     mx = fmaxf(mx, x);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = max_xor32(max_xor16(mx));
             const float m_new = fmaxf(m[rt], mx * fc);
             if (__any(m_new != m[rt])) {
                 const float corr = fast_exp2(m[rt] - m_new);
@@ -319,8 +320,7 @@ decode_part_kernel(DecodeArgs a)
     float lt[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        lt[rt] = l[rt] + __shfl_xor(l[rt], 16);
-        lt[rt] += __shfl_xor(lt[rt], 32);
+        lt[rt] = sum_xor32(sum_xor16(l[rt]));
     }
     __syncthreads();                                       // V^T regions are reused below
     float* slot0 = (float*)lds;

@@ -7,9 +7,9 @@
 
 namespace nxa {
 
-// Prefill: 128 queries x one q head per workgroup (4 waves x 32 rows), 64-key tiles.
+// Prefill: 128 queries x one q head per workgroup (4 waves x 32 rows); the key tile per
+// head dim is set with the kernel (attn_prefill.hip).
 constexpr int kPrefillBM = 128;
-constexpr int kPrefillBN = 64;
 constexpr int kPrefillThreads = 256;
 // Split-KV decode: 4 waves per (split, kv head, row group), 32 keys per wave step,
 // 16 query rows (n_query * G) per row tile and one or two row tiles per row group.

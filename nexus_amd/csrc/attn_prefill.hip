@@ -4,73 +4,112 @@
 // attn_flash.comp (src/gpu/shaders/attn_flash.comp:66-72, 121-159): query i sits at
 // absolute position q_base + i and sees keys [start, min(q_base + i, n_ctx - 1)].
 //
-// Design (one workgroup = 128 queries of one q head, 4 waves x 32 queries):
-//  * S^T = K Q^T on v_mfma_f32_32x32x16_f16.  A = K tile rows (keys) straight from LDS,
-//    B = Q^T held in registers for the whole key loop.  The D layout leaves each lane
-//    with one query column and 16 keys of a 32-key block, so the row max needs one
-//    cross-lane exchange (lane ^ 32) and P^T feeds the next MFMA without a shuffle.
-//  * O^T += V^T P^T on the same MFMA: A = V^T read from LDS, B = P^T from registers.
-//    V is transposed while it is staged into LDS (4 keys x 8 dims per thread, v_perm),
-//    and the keys of every 16-key group are stored in the order [0-3, 8-11, 4-7, 12-15]
-//    so that the 8 keys a lane contributes to P^T are one contiguous 16-byte LDS read.
-//  * Online softmax in fp32 registers, exp2 with log2(e) folded into the scale, lazy
-//    rescaling of O (only when a row max grows by more than 2^8).
-//  * K/V tiles (64 keys) are double-buffered in LDS; the next tile's global loads are
-//    issued before the current tile's MFMAs, one barrier per tile.
-//  * Blocks are remapped so each XCD owns whole KV heads (L2 reuse of K/V), and within a
-//    KV head the heaviest (latest) query blocks start first.
-//  * K/V/Q come in through raw buffer loads whose descriptor ends at the cache end (or
-//    the last query), so rows past it read as zero with no branch in the loop.
+// Design (one workgroup = 128 queries of one q head, 4 waves x 32 queries, 2 per CU):
+//  * K/V tiles (BN keys) go from HBM straight into LDS with buffer-load-to-LDS (16 bytes
+//    per lane, no VGPR staging, no transpose work) through a ring of STAGES buffers: the
+//    next STAGES - 1 tiles are in flight while the current one is consumed, one barrier
+//    per tile.  Each lane picks the
+//    global chunk whose LDS slot it writes, which XOR-swizzles the 16-byte chunks of every
+//    row so the operand reads below are free of bank conflicts.  Rows past the cache end
+//    read as zero through the buffer descriptor.
+//  * S^T = K Q^T on v_mfma_f32_32x32x16_f16: A = K rows from LDS, B = Q^T in registers for
+//    the whole key loop.  Q is pre-multiplied by scale * log2(e), and the accumulator
+//    starts at -m (the row's running max, a register splat), so the MFMA result is already
+//    s * scale * log2(e) - m and a probability is one exp2.
+//  * Online softmax in fp32, lazily rescaled: the running max only moves when a row's new
+//    scores exceed it by more than 2^8 (P stays <= 256, safe in f16), which is rare after
+//    the first tile; a per-row flag marks rows that have seen a visible key.  Row max: one
+//    v_max3 per two scores plus one v_permlane32_swap.  Row sums: v_dot2_f32_f16 on
+//    the packed f16 P, i.e. exactly the values the PV MFMA consumes.
+//  * O^T += V^T P^T on the same MFMA: B = P^T straight from the S^T registers (the D layout
+//    leaves lane (query n, half hh) with keys 8j + 4hh + (0..3)), A = V^T read from the
+//    row-major V tile with ds_read_b64_tr_b16: within 16 lanes the transposing read hands
+//    lane j four consecutive keys of dim d0 + j, two reads make an 8-key operand.
+//  * Work items are remapped so each XCD owns whole KV heads (L2 reuse of K/V); within a KV
+//    head the heaviest (latest) query blocks start first.
 //  * Optional split of the key range over n_splits workgroups (short chunks over a long
-//    cache, e.g. 512 queries after 4096 cached tokens).  Each split writes fp32 partials
-//    (acc, m, l) in the reference's split-K format; the decode path's combine kernel merges
-//    them with the LSE rule of qwen35_attn_comb.comp:16-40.
+//    cache).  Each split writes fp32 partials (acc, m, l) in the reference's split-K format;
+//    the decode path's combine kernel merges them with the LSE rule of
+//    qwen35_attn_comb.comp:16-40.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
 namespace nxa {
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Key tile and ring depth: the tiles in flight must cover the K/V load latency (a few us
+// from the MALL) while two workgroups share a CU's LDS.
+constexpr int prefill_bn(int hd) { return hd <= 128 ? 64 : 32; }
+constexpr int prefill_stages(int hd) { return 2 + 0 * hd; }
+
 template <int HD>
 struct PrefillLayout {
-    static constexpr int BN = kPrefillBN;
-    static constexpr int CPR = HD / 8;                        // 16-byte chunks per K row
-    static constexpr int K_BYTES = BN * HD * 2;               // K tile, row-major, swizzled
-    static constexpr int V_ROW = BN * 2;                      // V^T row (one dim, 64 keys)
-    static constexpr int V_BYTES = HD * V_ROW;
-    static constexpr int BUF_BYTES = K_BYTES + V_BYTES;
-    static constexpr int LDS_BYTES = 2 * BUF_BYTES;
-    // XOR mask that keeps a chunk inside its 8- or 16-chunk aligned group of the row
-    static constexpr int K_SWZ = (CPR % 16 == 0) ? 15 : 7;
-    static constexpr int K_LOADS = BN * CPR / kPrefillThreads;
-    static constexpr int V_BLOCKS = 16 * CPR;                 // (4-key quad, 8-dim chunk)
-    static constexpr int V_LOADS = (V_BLOCKS + kPrefillThreads - 1) / kPrefillThreads;
-    static_assert(K_LOADS >= 1, "K staging");
+    static constexpr int BN = prefill_bn(HD);
+    static constexpr int SB = BN / 32;                        // 32-key S^T blocks per tile
+    static constexpr int ROW = HD * 2;                        // bytes per K/V row
+    static constexpr int CPR = HD / 8;                        // 16-byte chunks per row
+    static constexpr int TILE = BN * ROW;                     // K (or V) tile bytes
+    static constexpr int BUF = 2 * TILE;                      // K + V
+    static constexpr int STAGES = prefill_stages(HD);
+    static constexpr int LDS_BYTES = STAGES * BUF;            // ring of STAGES tiles
+    static constexpr int LOADS = TILE / (kPrefillThreads * 16);   // 16-byte loads per thread per tile
+    // chunk swizzles stay inside aligned groups of 16 (or 8) chunks of a row
+    static constexpr int SWZ = (CPR % 16 == 0) ? 15 : 7;
+    static_assert(LOADS >= 1 && TILE % (kPrefillThreads * 16) == 0, "tile staging");
 };
 
-// LDS byte offset of K tile row `key`, 16-byte chunk `c` (XOR swizzle against bank conflicts).
+// Slot of global chunk c of K row r, and of V row r.  K: the 32 rows an A-operand read
+// touches (same chunk) spread over 16 slots.  V: a transposing read touches 4 consecutive
+// rows x 64 bytes per 32 lanes; XOR-ing the chunk with 4 * (row % 4) (rows a multiple of
+// 256 bytes apart, which share banks) or 4 * ((row / 2) % 2) (128- or 384-byte rows) puts
+// those segments on disjoint banks.
 template <int HD>
-__device__ __forceinline__ int k_off(int key, int c)
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & PrefillLayout<HD>::SWZ); }
+template <int HD>
+__device__ __forceinline__ int v_slot(int r, int c)
 {
-    using L = PrefillLayout<HD>;
-    return key * (HD * 2) + 16 * (c ^ (key & L::K_SWZ));
+    return c ^ ((PrefillLayout<HD>::ROW % 256 == 0) ? 4 * (r & 3) : 4 * ((r >> 1) & 1));
 }
 
-// LDS byte offset of V^T row `d`, 16-byte chunk `c` (8 key slots).
-__device__ __forceinline__ int vt_off(int d, int c)
+// Two waves per SIMD (two workgroups per CU) up to head_dim 128; larger head dims need one.
+constexpr int prefill_waves_per_simd(int hd) { return hd <= 128 ? 2 : 1; }
+
+// ds_read_b64_tr_b16 issued as inline asm.  The compiler does not see these reads as LDS
+// accesses that may alias the in-flight buffer-load-to-LDS of the next tile (the builtin
+// makes it drain all of them first, serialising the K/V load latency into every tile).
+// The caller waits for them with wait_lgkm0() on the result registers; LDS operations
+// complete in order, so untracked reads only ever make the compiler's own lgkmcnt waits
+// stronger.
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16_b64(const lds_u8* p)
 {
-    return d * (kPrefillBN * 2) + 16 * (c ^ ((d >> 1) & 7));
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF) : "memory");
+    return r;
+}
+
+// s_waitcnt lgkmcnt(0) that the compiler must order before every use of the four values.
+__device__ __forceinline__ void wait_lgkm0(u32x2& a, u32x2& b, u32x2& c, u32x2& d)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
 }
 
 template <int HD, bool Q_F32, bool O_F32, bool EXT>
-__global__ void __launch_bounds__(kPrefillThreads, HD <= 128 ? 2 : 1)
+__global__ void __launch_bounds__(kPrefillThreads, prefill_waves_per_simd(HD))
 prefill_kernel(PrefillArgs a)
 {
     using L = PrefillLayout<HD>;
-    constexpr int BM = kPrefillBM, BN = kPrefillBN;
+    constexpr int BM = kPrefillBM, BN = L::BN, SB = L::SB;
     constexpr int KSTEPS = HD / 16, DBLK = HD / 32;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    lds_u8* lds3 = (lds_u8*)lds;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index is uniform across the wave: readfirstlane lets the compiler keep
+    // per-wave bounds and branches scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 31, hh = lane >> 5;
 
     // ---- work item: (kv head, query block [heaviest first], q head in group, key split)
@@ -108,190 +147,241 @@ prefill_kernel(PrefillArgs a)
     if (EXT && a.sliding_window > 0 && a.q_base + w_first + 1 > a.sliding_window)
         w_klo = a.q_base + w_first + 1 - a.sliding_window;
 
-    // ---- Q^T operands: lane (query n, k-group hh) holds dims 16*ks + 8*hh .. +7
+    // ---- K/V tile staging: thread tid, load j fills LDS bytes 16 * (256 j + tid) of a tile
+    const uint32_t kv_bytes = (uint32_t)a.n_ctx * HD * 2;
+    const rsrc_t krs = make_rsrc_uniform(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    const rsrc_t vrs = make_rsrc_uniform(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    uint32_t koff[L::LOADS], voff[L::LOADS];              // byte offsets within a tile's rows
+#pragma unroll
+    for (int j = 0; j < L::LOADS; ++j) {
+        const int b = 16 * (kPrefillThreads * j + tid);
+        const int row = b / L::ROW, slot = (b % L::ROW) / 16;
+        koff[j] = (uint32_t)(row * L::ROW + 16 * k_slot<HD>(row, slot));
+        voff[j] = (uint32_t)(row * L::ROW + 16 * v_slot<HD>(row, slot));
+    }
+    auto issue_tile = [&](int t, int buf) {
+        const uint32_t base = (uint32_t)(t * BN) * L::ROW;
+        lds_u8* kl = lds3 + buf * L::BUF + 1024 * wave;
+        lds_u8* vl = kl + L::TILE;
+#pragma unroll
+        for (int j = 0; j < L::LOADS; ++j) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (void __attribute__((address_space(3)))*)(kl + 4096 * j), 16,
+                                                     (int)(base + koff[j]), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (void __attribute__((address_space(3)))*)(vl + 4096 * j), 16,
+                                                     (int)(base + voff[j]), 0, 0, 0);
+        }
+    };
+    // ring prologue: tiles t_begin .. t_begin + STAGES - 2 in flight
+#pragma unroll
+    for (int st = 0; st + 1 < L::STAGES; ++st)
+        if (t_begin + st < t_end) issue_tile(t_begin + st, st);
+
+    // ---- Q^T operands, pre-scaled: lane (query n, k-group hh) holds dims 16*ks + 8*hh .. +7
+    const float qscale = EXT ? a.scale : a.scale_log2;
     constexpr uint32_t QE = Q_F32 ? 4u : 2u;
     f16x8 qt[KSTEPS];
     {
         const size_t row_bytes = (size_t)a.n_q_heads * HD * QE;
         const int blk_rows = min(BM, a.n_query - q0);
-        const rsrc_t qr = make_rsrc((const char*)a.q + (size_t)q0 * row_bytes, (uint32_t)(blk_rows * row_bytes));
+        const rsrc_t qr = make_rsrc_uniform((const char*)a.q + (size_t)q0 * row_bytes, (uint32_t)(blk_rows * row_bytes));
         const uint32_t qoff = (uint32_t)((32 * wave + n) * row_bytes + ((size_t)h * HD + 8 * hh) * QE);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
+            float x[8];
             if constexpr (Q_F32) {
                 const f32x4 x0 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks));
                 const f32x4 x1 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks + 16));
-                qt[ks] = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x[i] = x0[i];
+                    x[4 + i] = x1[i];
+                }
             } else {
-                qt[ks] = as_f16x8(buf_load16(qr, qoff + 32 * ks));
+                const f16x8 hq = as_f16x8(buf_load16(qr, qoff + 32 * ks));
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = (float)hq[i];
             }
+            qt[ks] = cvt_f16x8(x[0] * qscale, x[1] * qscale, x[2] * qscale, x[3] * qscale, x[4] * qscale,
+                               x[5] * qscale, x[6] * qscale, x[7] * qscale);
         }
     }
 
-    // K/V of this kv head; the descriptors end at row n_ctx
-    const uint32_t kv_bytes = (uint32_t)a.n_ctx * HD * 2;
-    const rsrc_t krs = make_rsrc(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
-    const rsrc_t vrs = make_rsrc(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
-    u32x4 kreg[L::K_LOADS];
-    u32x4 vreg[L::V_LOADS][4];
-
-    // global -> registers for tile t
-    auto load_tile = [&](int t) {
-        const uint32_t key0 = (uint32_t)(t * BN);
+    // ---- per-lane LDS read offsets (bytes within a tile)
+    // K A operand, block sb, k-step ks: row 32 sb + n, chunk 2 ks + hh
+    int ka_off[KSTEPS];
 #pragma unroll
-        for (int i = 0; i < L::K_LOADS; ++i) {
-            const int idx = tid + kPrefillThreads * i;
-            const int key = idx / L::CPR, c = idx % L::CPR;
-            kreg[i] = buf_load16(krs, ((key0 + key) * HD + 8 * c) * 2);
+    for (int ks = 0; ks < KSTEPS; ++ks) ka_off[ks] = n * L::ROW + 16 * k_slot<HD>(n, 2 * ks + hh);
+    // V^T transposing reads: source lane i = lane & 15 of each 16-lane group addresses
+    // V[kb + i/4][d0 + 4 (i%4)], kb = 32 sb + 16 j + 4 hh (+8 for the second half),
+    // d0 = 32 db + 16 ((lane >> 4) & 1); the swizzle depends on the row only through
+    // (4 hh + i/4) mod 4, which is the same for every (sb, j, half).
+    int vt_off[DBLK];
+    {
+        const int i = lane & 15;
+        const int rr = 4 * hh + (i >> 2);                 // row within a 16-key group (mod 16)
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+            const int dim = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
+            vt_off[db] = rr * L::ROW + 16 * v_slot<HD>(rr, dim >> 3) + 8 * ((dim >> 2) & 1);
         }
-#pragma unroll
-        for (int j = 0; j < L::V_LOADS; ++j) {
-            const int blk = tid + kPrefillThreads * j;
-            if (L::V_BLOCKS % kPrefillThreads == 0 || blk < L::V_BLOCKS) {
-                const int kq = blk & 15, cc = blk >> 4;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    vreg[j][i] = buf_load16(vrs, ((key0 + 4 * kq + i) * HD + 8 * cc) * 2);
-            }
-        }
-    };
-    // registers -> LDS buffer `buf` (K as is, V transposed + key-permuted)
-    auto store_tile = [&](int buf) {
-        uint8_t* kl = lds + buf * L::BUF_BYTES;
-        uint8_t* vl = kl + L::K_BYTES;
-#pragma unroll
-        for (int i = 0; i < L::K_LOADS; ++i) {
-            const int idx = tid + kPrefillThreads * i;
-            const int key = idx / L::CPR, c = idx % L::CPR;
-            *(u32x4*)(kl + k_off<HD>(key, c)) = kreg[i];
-        }
-#pragma unroll
-        for (int j = 0; j < L::V_LOADS; ++j) {
-            const int blk = tid + kPrefillThreads * j;
-            if (L::V_BLOCKS % kPrefillThreads == 0 || blk < L::V_BLOCKS) {
-                const int kq = blk & 15, cc = blk >> 4;
-                const int q4 = kq & 3;
-                const int pos = ((q4 & 1) << 1) | (q4 >> 1);      // slot quad within the 16-key group
-                const int c = 2 * (kq >> 2) + (pos >> 1);
-                const int half = (pos & 1) * 8;
-#pragma unroll
-                for (int dd = 0; dd < 8; ++dd) {
-                    const int d = 8 * cc + dd;
-                    const int wj = dd >> 1;
-                    const uint32_t sel = (dd & 1) ? kSelHi : kSelLo;
-                    u32x2 val;
-                    val[0] = perm_b32(vreg[j][1][wj], vreg[j][0][wj], sel);
-                    val[1] = perm_b32(vreg[j][3][wj], vreg[j][2][wj], sel);
-                    *(u32x2*)(vl + vt_off(d, c) + half) = val;
-                }
-            }
-        }
-    };
+    }
 
     f32x16 o[DBLK];
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[db][v] = 0.f;
-    float m_used = kNegBig;     // log2 units
-    float l_part = 0.f;         // this lane's share of the row sum (its 16 keys per block)
-    const float fc = EXT ? 1.f : a.scale_log2;
+    // running max m_used (log2 units of the pre-scaled score) and its negated splat, which
+    // seeds every S^T accumulator; `seen` marks a row that has had a visible key
+    float m_used = 0.f;
+    bool seen = false;
+    f32x16 negm;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) negm[v] = 0.f;
+    float l_part = 0.f;                                   // this lane's share of the row sum
+    const f16x2 ones = {(_Float16)1.f, (_Float16)1.f};
 
-    if (t_begin < t_end) {
-        load_tile(t_begin);
-        store_tile(0);
-    }
-    __syncthreads();
-
+    constexpr int LOADS_PER_TILE = 2 * L::LOADS;
+    // s_waitcnt immediate for vmcnt(n) (expcnt and lgkmcnt left at their maxima)
+    constexpr int kWaitLater = ((L::STAGES - 2) * LOADS_PER_TILE & 15) |
+                               (((L::STAGES - 2) * LOADS_PER_TILE >> 4) << 14) | 0x0f70;
+    static_assert((L::STAGES - 2) * LOADS_PER_TILE < 64, "vmcnt range");
     for (int t = t_begin; t < t_end; ++t) {
-        const int buf = (t - t_begin) & 1;
-        const bool has_next = t + 1 < t_end;
-        if (has_next) load_tile(t + 1);
+        const int buf = (t - t_begin) % L::STAGES;
+        // this thread's tile-t loads have landed once at most the later tiles' loads remain
+        if (t + L::STAGES - 2 < t_end) __builtin_amdgcn_s_waitcnt(kWaitLater);
+        else __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();                                  // ... everyone's; the oldest buffer is free
+        if (t + L::STAGES - 1 < t_end) issue_tile(t + L::STAGES - 1, (buf + L::STAGES - 1) % L::STAGES);
         const int key0 = t * BN;
-        if (wave_active && key0 <= w_khi && key0 + BN - 1 >= w_klo) {
-            const uint8_t* kl = lds + buf * L::BUF_BYTES;
-            const uint8_t* vl = kl + L::K_BYTES;
-            f32x16 s[2];
+        if (!(wave_active && key0 <= w_khi && key0 + BN - 1 >= w_klo)) continue;
+        const lds_u8* kl = lds3 + buf * L::BUF;
+        const lds_u8* vl = kl + L::TILE;
+
+        // S^T = K Q^T (+ -m seed).  All K operands of the tile are read first, then the
+        // MFMAs run with the independent accumulators interleaved; the scheduling barriers
+        // keep the compiler from pairing every read with its MFMA (a serial chain of LDS
+        // and MFMA latencies).
+        f16x8 ka[SB][KSTEPS];
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
+        for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) s[sb][v] = 0.f;
-                const int kr = 32 * sb + n;
+            for (int sb = 0; sb < SB; ++sb)
+                ka[sb][ks] = *(const f16x8 __attribute__((address_space(3)))*)(kl + 32 * sb * L::ROW + ka_off[ks]);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x16 s[SB];
 #pragma unroll
-                for (int ks = 0; ks < KSTEPS; ++ks) {
-                    const f16x8 ka = *(const f16x8*)(kl + k_off<HD>(kr, 2 * ks + hh));
-                    s[sb] = mfma32x32x16(ka, qt[ks], s[sb]);
-                }
+        for (int sb = 0; sb < SB; ++sb) s[sb] = EXT ? f32x16{} : negm;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+            for (int sb = 0; sb < SB; ++sb) s[sb] = mfma32x32x16(ka[sb][ks], qt[ks], s[sb]);
+        // V^T operands of the first 32-key block, read while the S MFMAs execute
+        u32x2 vr[SB][DBLK][2][2];
+        auto read_vt = [&](auto SBc) {
+            constexpr int sb = decltype(SBc)::value;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                const lds_u8* vb = vl + vt_off[db];
+                vr[sb][db][0][0] = ds_read_tr16_b64<(32 * sb + 0) * L::ROW>(vb);
+                vr[sb][db][0][1] = ds_read_tr16_b64<(32 * sb + 8) * L::ROW>(vb);
+                vr[sb][db][1][0] = ds_read_tr16_b64<(32 * sb + 16) * L::ROW>(vb);
+                vr[sb][db][1][1] = ds_read_tr16_b64<(32 * sb + 24) * L::ROW>(vb);
             }
-            const bool need_mask = (key0 + BN - 1 > a.q_base + w_first) || (key0 + BN > a.n_ctx) ||
-                                   (EXT && a.sliding_window > 0 &&
-                                    key0 < a.q_base + w_last + 1 - a.sliding_window);
-            float mx = -INFINITY;
+        };
+        // wait for this block's reads; the "+v" operands order the wait before every use
+        auto wait_vt = [&](auto SBc) {
+            constexpr int sb = decltype(SBc)::value;
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
+            for (int db = 0; db < DBLK; ++db)
+                wait_lgkm0(vr[sb][db][0][0], vr[sb][db][0][1], vr[sb][db][1][0], vr[sb][db][1][1]);
+        };
+        read_vt(std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        // scores -> log2 domain relative to m_used, masked
+        const bool need_mask = (key0 + BN - 1 > a.q_base + w_first) || (key0 + BN > a.n_ctx) ||
+                               (EXT && a.sliding_window > 0 && key0 < a.q_base + w_last + 1 - a.sliding_window);
+        if constexpr (EXT) {
+#pragma unroll
+            for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     float x = s[sb][v];
-                    if constexpr (EXT) {
-                        x *= a.scale;
-                        if (a.softcap > 0.f) x = a.softcap * tanhf(x / a.softcap);
-                        x *= kLog2e;
-                    }
-                    if (need_mask) {
-                        const int key = key0 + 32 * sb + 8 * (v >> 2) + 4 * hh + (v & 3);
-                        bool vis = key <= qpos && key < a.n_ctx;
-                        if (EXT && a.sliding_window > 0) vis = vis && key >= qpos + 1 - a.sliding_window;
-                        if (!vis) x = -INFINITY;
-                    }
-                    s[sb][v] = x;
-                    mx = fmaxf(mx, x);
+                    if (a.softcap > 0.f) x = a.softcap * tanhf(x / a.softcap);
+                    s[sb][v] = x * kLog2e - m_used;
                 }
-            }
-            mx = fmaxf(mx, xor32(mx));
-            const float mt = mx * fc;
-            const bool need = mt > m_used + kRescaleThresh;
-            if (__any(need)) {
-                const float m_new = need ? mt : m_used;
-                const float corr = fast_exp2(m_used - m_new);
-                l_part *= corr;
+        }
+        if (need_mask) {                                  // wave-uniform: diagonal / boundary tiles
 #pragma unroll
-                for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) o[db][v] *= corr;
-                m_used = m_new;
-            }
-            f16x8 pb[2][2];
-            float lsum = 0.f;
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
-                float p[16];
+            for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    p[v] = fast_exp2(fmaf(s[sb][v], fc, -m_used));
-                    lsum += p[v];
+                    const int key = key0 + 32 * sb + 8 * (v >> 2) + 4 * hh + (v & 3);
+                    bool vis = key <= qpos && key < a.n_ctx;
+                    if (EXT && a.sliding_window > 0) vis = vis && key >= qpos + 1 - a.sliding_window;
+                    s[sb][v] = vis ? s[sb][v] : -INFINITY;
                 }
-                pb[sb][0] = cvt_f16x8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
-                pb[sb][1] = cvt_f16x8(p[8], p[9], p[10], p[11], p[12], p[13], p[14], p[15]);
-            }
-            l_part += lsum;
-#pragma unroll
-            for (int db = 0; db < DBLK; ++db) {
-                const int d = 32 * db + n;
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const f16x8 va = *(const f16x8*)(vl + vt_off(d, 2 * (2 * sb + j) + hh));
-                        o[db] = mfma32x32x16(va, pb[sb][j], o[db]);
-                    }
-            }
         }
-        if (has_next) store_tile(buf ^ 1);
-        __syncthreads();
+        float mx = -INFINITY;
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int v = 0; v < 16; v += 2) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[sb][v], s[sb][v + 1]));
+        mx = max_xor32(mx);
+        // lazy rescale: a row moves its max when it first sees a key, or when its scores
+        // exceed the current max by more than 2^8
+        const bool need = seen ? (mx > kRescaleThresh) : (mx > -INFINITY);
+        if (__any(need)) {
+            const float d = need ? mx : 0.f;
+            const float corr = fast_exp2(-d);
+            m_used += d;
+            seen = seen || need;
+            l_part *= corr;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) o[db] *= corr;
+#pragma unroll
+            for (int sb = 0; sb < SB; ++sb) s[sb] -= d;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) negm[v] = -m_used;
+        }
+        // P = exp2(S), packed to f16 for the PV MFMA; row sums from the packed values
+        f16x8 pb[SB][2];
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float p[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) p[i] = fast_exp2(s[sb][8 * j + i]);
+                const f16x8 ph = cvt_f16x8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+                pb[sb][j] = ph;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const f16x2 pp = {ph[2 * i], ph[2 * i + 1]};
+                    l_part = __builtin_amdgcn_fdot2(pp, ones, l_part, false);
+                }
+            }
+        // O^T += V^T P^T, the DBLK independent accumulators interleaved; the next block's V^T
+        // operands are read while the current block's MFMAs execute
+        auto pv = [&](auto SBc) {
+            constexpr int sb = decltype(SBc)::value;
+            wait_vt(SBc);
+            if constexpr (sb + 1 < SB) read_vt(std::integral_constant<int, sb + 1>{});
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int db = 0; db < DBLK; ++db) {
+                    const f16x8 va = __builtin_bit_cast(
+                        f16x8, u32x4{vr[sb][db][j][0][0], vr[sb][db][j][0][1], vr[sb][db][j][1][0], vr[sb][db][j][1][1]});
+                    o[db] = mfma32x32x16(va, pb[sb][j], o[db]);
+                }
+        };
+        pv(std::integral_constant<int, 0>{});
+        if constexpr (SB > 1) pv(std::integral_constant<int, 1>{});
     }
 
     // ---- epilogue: lane (query n, hh) holds dims 32*db + 8*a4 + 4*hh + (0..3)
-    float l_tot = l_part + xor32(l_part);
+    float l_tot = sum_xor32(l_part);
     auto store_out = [&](float inv) {
         const size_t obase = ((size_t)qrow * a.n_q_heads + h) * HD;
 #pragma unroll
@@ -330,7 +420,9 @@ prefill_kernel(PrefillArgs a)
                 *(f32x2*)(pr + dim) = f32x2{o[db][4 * a4], o[db][4 * a4 + 1]};
                 *(f32x2*)(pr + dim + 2) = f32x2{o[db][4 * a4 + 2], o[db][4 * a4 + 3]};
             }
-        if (hh == 0) *(f32x2*)(pr + HD) = f32x2{m_used * kLn2, l_tot};   // m in natural-log units
+        // m in natural-log units; a row with no visible key in this split carries the
+        // reference's initial max and l = 0
+        if (hh == 0) *(f32x2*)(pr + HD) = f32x2{seen ? m_used * kLn2 : kNegBig, l_tot};
     }
 }
 
