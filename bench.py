@@ -138,24 +138,41 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False) -> dict:
 
 
 def copy_calibration(steps: int, warmup: int, nbytes: int = 256 << 20) -> None:
-    """A plain device-to-device copy of known size: the reference point that scales the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes nbytes)."""
+    """A plain elementwise copy of known size (torch.mul by 1 over float32: each launch reads
+    and writes nbytes): the reference point that scales the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE counters."""
     import torch
 
-    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_()
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
     dst = torch.empty_like(src)
     for _ in range(warmup):
-        dst.copy_(src)
+        torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s0.record()
     for _ in range(steps):
-        dst.copy_(src)
+        torch.mul(src, 1.0, out=dst)
     s1.record()
     s1.synchronize()
     ms = s0.elapsed_time(s1) / steps
     log(f"[bench] copy {nbytes >> 20} MiB: {ms * 1e3:.1f} us/launch, {2 * nbytes / (ms * 1e-3) / 1e9:.0f} GB/s "
         f"(read+write), {nbytes / 1024:.0f} KiB read and written per launch")
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch of a config's dominant kernel, from the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE runs recorded in profiles/traffic.json (each counter scaled by its reading
+    for the calibration copy).  None when no measurement is recorded."""
+    import json
+
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())[name]
+        return float(rec["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(target_s: float = 10.0) -> dict:
@@ -272,8 +289,10 @@ def main() -> int:
                    "head_dim": c2["hd"], "n_query": c2["nq"], "q_base_pos": c2["base"], "n_ctx": c2["n_ctx"],
                    "kv_splits": head["splits"], "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": head["tflops"] / MFMA_F16_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "prefill_kernel<128,f16,f16> + combine_kernel (whole call timed)",
+                     "unit": "TFLOP/s", "frac": head["tflops"] / MFMA_F16_PEAK_TFLOPS,
+                     "traffic": measured_traffic("cfg2"),
+                     "kernel": "nxa::prefill_kernel<128, f16 Q, f16 O> (one launch per call, timed with "
+                               "HIP events on its stream)",
                      "algorithmic_gflop_per_call": head["gflop"]},
         "cpu_baseline": cpu,
         "extra": extra,
