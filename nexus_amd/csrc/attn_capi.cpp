@@ -155,11 +155,6 @@ size_t decode_ws_bytes(const nexus_attn_desc* d, int n_splits)
     return nxa::ws_partial_bytes((long long)d->n_query * d->n_q_heads, n_splits, d->head_dim);
 }
 
-long long prefill_qblocks(const nexus_attn_desc* d)
-{
-    return (d->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
-}
-
 size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
 {
     return nxa::ws_partial_bytes((long long)d->n_query * d->n_q_heads, splits, d->head_dim);
@@ -183,6 +178,30 @@ int prefill_splits(const nexus_attn_desc* d)
     if (s > tiles / 4) s = tiles / 4;
     if (s > 16) s = 16;
     return s < 1 ? 1 : (int)s;
+}
+
+// Prefill kernel choice.  Plain causal shapes (no softcap, no sliding window) at the head
+// dims the pipelined kernel covers take it, unsplit: 128-row blocks (KS = 1), or 64-row
+// blocks with the key range split over two waves of the workgroup (KS = 2) when 128-row
+// blocks leave CUs without a workgroup.  Other shapes take prefill_kernel with its split rule.
+struct PrefillPlan {
+    bool wide;
+    int ks;
+    int splits;
+};
+
+PrefillPlan prefill_plan(const nexus_attn_desc* d)
+{
+    PrefillPlan p{false, 1, 1};
+    if (!is_ext(d) && nxa::prefill_wide_supported(d->head_dim)) {
+        p.wide = true;
+        const long long rows1 = nxa::prefill_wide_rows(1);
+        const long long wgs1 = (long long)d->n_q_heads * ((d->n_query + rows1 - 1) / rows1);
+        p.ks = wgs1 < device_cus() ? 2 : 1;
+        return p;
+    }
+    p.splits = prefill_splits(d);
+    return p;
 }
 
 bool small_query_path(const nexus_attn_desc* d)
@@ -280,7 +299,7 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
 {
     if (check_desc(desc) != NEXUS_OK) return 0;
     if (small_query_path(desc)) return decode_ws_bytes(desc, default_decode_splits(desc));
-    const int s = prefill_splits(desc);
+    const int s = prefill_plan(desc).splits;
     if (s <= 1) return 0;
     return prefill_split_ws_bytes(desc, s);
 }
@@ -302,7 +321,8 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
             return run_decode(desc, q, k, v, out, (float*)workspace, splits, s);
     }
 
-    int splits = prefill_splits(desc);
+    const PrefillPlan plan = prefill_plan(desc);
+    int splits = plan.splits;
     if (splits > 1 && (!workspace || workspace_bytes < prefill_split_ws_bytes(desc, splits))) splits = 1;
 
     nxa::PrefillArgs a{};
@@ -322,13 +342,15 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.scale = eff_scale(desc);
     a.scale_log2 = a.scale * 1.4426950408889634f;
     a.softcap = desc->softcap;
-    a.n_qblocks = (int)prefill_qblocks(desc);
+    const long long rows = plan.wide ? nxa::prefill_wide_rows(plan.ks) : nxa::kPrefillBM;
+    a.n_qblocks = (int)((desc->n_query + rows - 1) / rows);
     a.n_splits = splits;
     const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
     if (items > INT_MAX) return fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
-    hipError_t e = nxa::launch_prefill(a, desc->head_dim, desc->q_dtype == NEXUS_DT_F32,
-                                       desc->o_dtype == NEXUS_DT_F32, is_ext(desc), s);
+    const bool q32 = desc->q_dtype == NEXUS_DT_F32, o32 = desc->o_dtype == NEXUS_DT_F32;
+    hipError_t e = plan.wide ? nxa::launch_prefill_wide(a, desc->head_dim, plan.ks, q32, o32, s)
+                             : nxa::launch_prefill(a, desc->head_dim, q32, o32, is_ext(desc), s);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
     if (splits > 1) {
         const int rc2 = launch_combine_for(desc, (float*)workspace, out, splits, s);

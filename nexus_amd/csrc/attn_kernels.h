@@ -11,6 +11,9 @@ namespace nxa {
 // head dim is set with the kernel (attn_prefill.hip).
 constexpr int kPrefillBM = 128;
 constexpr int kPrefillThreads = 256;
+// Pipelined prefill (attn_prefill_wide.hip): 32 query rows per wave, 4 waves per workgroup
+// as 4 row waves (KS = 1, 128 rows) or 2 row waves x 2 key groups (KS = 2, 64 rows).
+constexpr int kWideRowsPerWave = 32;
 // Split-KV decode: 4 waves per (split, kv head, row group), 32 keys per wave step,
 // 16 query rows (n_query * G) per row tile and one or two row tiles per row group.
 constexpr int kDecodeThreads = 256;
@@ -70,6 +73,12 @@ inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.
 hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                           hipStream_t stream);
+// Wide prefill: plain causal shapes (no softcap, no sliding window, one key split), head dims
+// prefill_wide_supported() accepts; n_qblocks counts prefill_wide_rows(ks)-row blocks.
+bool prefill_wide_supported(int head_dim);
+int prefill_wide_rows(int ks);
+hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32,
+                               hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);
 hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream);

@@ -1,0 +1,584 @@
+// nexus_amd/csrc/attn_prefill_wide.hip -- software-pipelined causal GQA flash-attention
+// prefill for gfx950.
+//
+// Semantics are those of prefill_kernel (attn_prefill.hip), i.e. Transformer::attn_batch_cpu
+// (src/model/transformer.h:8653-8685) and attn_flash.comp (src/gpu/shaders/attn_flash.comp:
+// 66-72, 121-159): query i sits at absolute position q_base + i and sees keys
+// [0, min(q_base + i, n_ctx - 1)].  This kernel takes the plain causal shapes (no logit
+// softcap, no sliding window, no key split across workgroups); prefill_kernel keeps those.
+//
+// Design:
+//  * A wave owns 32 query rows; two waves per SIMD.  Workgroup = 4 waves.  KS = 1: four row
+//    waves (128 query rows) share every K/V tile.  KS = 2: two row waves x two key groups
+//    (64 rows); key group g takes the tiles t = g (mod 2) and the groups' (O, m, l) merge
+//    through LDS at the end -- for short chunks, where 128-row blocks leave CUs idle.
+//  * Software pipeline over key tiles.  While the MFMAs of S(t+1) = K(t+1) Q^T run, the VALU
+//    turns S(t) into P(t) (exp2, f16 pack, row sums); while the MFMAs of O^T += V(t)^T P(t)^T
+//    run, the VALU takes the row max of S(t+1).  A wave issues in order, so its VALU work
+//    only overlaps its own MFMAs when the two alternate in program order: each MFMA slot is
+//    written with its share of VALU work and LDS reads and fenced with sched_barrier.  The
+//    two S^T tiles swap roles from step to step (loop unrolled by two, no copies).
+//  * Every wave of a workgroup runs the same steps: no per-wave branch in the loop body, so
+//    O, Q^T and both S^T tiles keep fixed registers (the last step is peeled).
+//  * K runs one tile ahead of V in the LDS ring: during step s the ring holds K(s+1) and V(s)
+//    and receives K(s+2) and V(s+1) (buffer-load-to-LDS of XOR-swizzled 16-byte chunks, the
+//    slot layout of prefill_kernel), one barrier per step.
+//  * S^T = K Q^T with Q pre-scaled by scale * log2(e) and the accumulator seeded with -m, so a
+//    probability is one exp2; the running max moves lazily (only past a 2^8 margin), the row
+//    max is v_max3 + v_permlane32_swap, row sums are v_dot2 over the packed f16 P.
+#include "attn_common.h"
+#include "attn_kernels.h"
+
+namespace nxa {
+
+namespace {
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+template <int HD, int KS>
+struct WideLayout {
+    // keys per tile: 32 at head dim 128 keeps two S^T tiles, O and Q^T of a 32-row wave in
+    // the 256 registers of two waves per SIMD
+    static constexpr int BN = HD >= 128 ? 32 : 64;
+    static constexpr int SB = BN / 32;                          // 32-key S^T blocks per tile
+    static constexpr int NB = kWideRowsPerWave / 32;            // 32-row blocks per wave
+    static constexpr int RWAVES = 4 / KS;                       // row waves per workgroup
+    static constexpr int BM = RWAVES * kWideRowsPerWave;        // query rows per workgroup
+    static constexpr int ROW = HD * 2;                          // bytes per K/V row
+    static constexpr int CPR = HD / 8;                          // 16-byte chunks per row
+    static constexpr int TILE = BN * ROW;
+    static constexpr int SLOTS = 2 * KS;                        // ring slots per operand
+    static constexpr int VBASE = SLOTS * TILE;
+    static constexpr int RING_BYTES = 2 * SLOTS * TILE;
+    // KS = 2: per row wave, O of both row blocks (16 registers x 64 lanes per 32-dim block)
+    // and (m, l) per row block
+    static constexpr int MERGE_FLOATS = NB * (HD / 32) * 16 * 64 + NB * 2 * 64;
+    static constexpr int MERGE_BYTES = KS > 1 ? RWAVES * MERGE_FLOATS * 4 : 0;
+    static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
+    static constexpr int LOADS = TILE / (kPrefillThreads * 16); // 16-byte loads per thread per tile
+    static constexpr int SWZ = (CPR % 16 == 0) ? 15 : 7;
+    static_assert(LOADS >= 1 && TILE % (kPrefillThreads * 16) == 0, "tile staging");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+};
+
+// Slot of global chunk c of K row r and of V row r (the conflict-free layouts of
+// prefill_kernel: a K operand read spreads its 32 rows over 16 slots; a transposing V read
+// puts its 4 rows x 64 bytes per 32 lanes on disjoint banks).
+template <int HD>
+__device__ __forceinline__ int wk_slot(int r, int c) { return c ^ (r & WideLayout<HD, 1>::SWZ); }
+template <int HD>
+__device__ __forceinline__ int wv_slot(int r, int c)
+{
+    return c ^ ((WideLayout<HD, 1>::ROW % 256 == 0) ? 4 * (r & 3) : 4 * ((r >> 1) & 1));
+}
+
+// ds_read_b64_tr_b16 as inline asm: the builtin makes the compiler drain every in-flight
+// buffer-load-to-LDS first (it cannot tell the ring slots apart).  The reads are waited for
+// explicitly (wait_lgkm); LDS operations of a wave complete in order.
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16(const lds_u8* p)
+{
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF) : "memory");
+    return r;
+}
+// s_waitcnt lgkmcnt(N), ordered before every use of the two registers
+template <int N>
+__device__ __forceinline__ void wait_lgkm(u32x2& a, u32x2& b)
+{
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
+// f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+constexpr int kWaitVm0 = 0x0f70;
+
+}  // namespace
+
+template <int HD, int KS, bool Q_F32, bool O_F32>
+__global__ void __launch_bounds__(kPrefillThreads, kWideRowsPerWave == 32 ? 2 : 1)
+prefill_wide_kernel(PrefillArgs a)
+{
+    using L = WideLayout<HD, KS>;
+    constexpr int BN = L::BN, SB = L::SB, NB = L::NB, BM = L::BM;
+    constexpr int KSTEPS = HD / 16, DBLK = HD / 32;
+    constexpr int RPW = kWideRowsPerWave;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    lds_u8* lds3 = (lds_u8*)lds;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31, hh = lane >> 5;
+    const int rw = wave % L::RWAVES, kg = wave / L::RWAVES;
+
+    // ---- work item: (kv head, query block [heaviest first], q head in group)
+    const int item = xcd_remap(blockIdx.x, a.n_items);
+    const int per_kv = a.group * a.n_qblocks;
+    const int kvh = item / per_kv;
+    const int r = item - kvh * per_kv;
+    const int qb = a.n_qblocks - 1 - r / a.group;
+    const int g = r - (r / a.group) * a.group;
+    const int h = kvh * a.group + g;
+
+    const int q0 = qb * BM;
+    const int k_hi = min(a.q_base + min(q0 + BM, a.n_query) - 1, a.n_ctx - 1);
+    const int t_end = k_hi / BN + 1;                     // the workgroup's tiles: 0 .. t_end - 1
+    const int n_steps = (t_end + KS - 1) / KS;
+
+    // ---- this wave's rows.  Every wave runs all n_steps steps of the workgroup (same trip
+    // count, no per-wave branches in the loop): tiles past a wave's diagonal are fully masked
+    // for it, and key group 1 of an odd tile count takes one tile past the last (loaded like
+    // any other, zero past the cache end, fully masked by causality).
+    const int w_first = q0 + RPW * rw;
+    const bool wave_active = w_first < a.n_query;
+    int qpos[NB];
+#pragma unroll
+    for (int rb = 0; rb < NB; ++rb) qpos[rb] = a.q_base + w_first + 32 * rb + n;
+
+    // ---- K/V staging: thread tid, load j fills LDS bytes 16 * (256 j + tid) of a tile
+    const uint32_t kv_bytes = (uint32_t)a.n_ctx * HD * 2;
+    const rsrc_t krs = make_rsrc_uniform(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    const rsrc_t vrs = make_rsrc_uniform(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
+    // The swizzle depends on the row only modulo 16, and load j + 1 lands 4096 bytes (a
+    // multiple of 16 rows) after load j, so one per-lane offset serves every load (load j
+    // adds 4096 j).
+    static_assert((kPrefillThreads * 16 / L::ROW) % 16 == 0, "swizzle period");
+    uint32_t koff, voff;
+    {
+        const int b = 16 * tid;
+        const int row = b / L::ROW, slot = (b % L::ROW) / 16;
+        koff = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row, slot));
+        voff = (uint32_t)(row * L::ROW + 16 * wv_slot<HD>(row, slot));
+    }
+    // tiles of step `st`: tile st * KS + i goes to slot (st & 1) * KS + i
+    auto issue = [&](int st, bool k_side) {
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const int t = st * KS + i;
+            {
+                const int base = t * BN * L::ROW;
+                lds_u8* dst = lds3 + (k_side ? 0 : L::VBASE) + ((st & 1) * KS + i) * L::TILE + 1024 * wave;
+#pragma unroll
+                for (int j = 0; j < L::LOADS; ++j)
+                    // the whole offset in the vector operand: the descriptor's range check
+                    // (zeros past the cache end) covers it
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        k_side ? krs : vrs, (void __attribute__((address_space(3)))*)(dst + 4096 * j), 16,
+                        (int)(k_side ? koff : voff) + base + 4096 * j, 0, 0, 0);
+            }
+        }
+    };
+    issue(0, true);
+    issue(0, false);
+    if (n_steps > 1) issue(1, true);
+
+    // ---- Q^T operands of both row blocks, pre-scaled by scale * log2(e): lane (row n, k-group
+    // hh) holds dims 16 ks + 8 hh .. +7
+    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
+    f16x8 qt[NB][KSTEPS];
+    {
+        const size_t row_bytes = (size_t)a.n_q_heads * HD * QE;
+        const int blk_rows = min(BM, a.n_query - q0);
+        const rsrc_t qr = make_rsrc_uniform((const char*)a.q + (size_t)q0 * row_bytes, (uint32_t)(blk_rows * row_bytes));
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb) {
+            const uint32_t qoff = (uint32_t)((RPW * rw + 32 * rb + n) * row_bytes + ((size_t)h * HD + 8 * hh) * QE);
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                float x[8];
+                if constexpr (Q_F32) {
+                    const f32x4 x0 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks));
+                    const f32x4 x1 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks + 16));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        x[i] = x0[i];
+                        x[4 + i] = x1[i];
+                    }
+                } else {
+                    const f16x8 hq = as_f16x8(buf_load16(qr, qoff + 32 * ks));
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) x[i] = (float)hq[i];
+                }
+                const float qs = a.scale_log2;
+                qt[rb][ks] = cvt_f16x8(x[0] * qs, x[1] * qs, x[2] * qs, x[3] * qs, x[4] * qs, x[5] * qs,
+                                       x[6] * qs, x[7] * qs);
+            }
+        }
+    }
+
+    // ---- per-lane LDS read offsets within a tile
+    // K operand of block sb, k-step ks: row 32 sb + n, chunk 2 ks + hh
+    int ka_off[KSTEPS];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) ka_off[ks] = n * L::ROW + 16 * wk_slot<HD>(n, 2 * ks + hh);
+    // V^T transposing reads: source lane i = lane & 15 of each 16-lane group addresses
+    // V[kb + i/4][d0 + 4 (i%4)], kb = 32 sb + 16 j + 4 hh (+8 for the second read),
+    // d0 = 32 db + 16 ((lane >> 4) & 1); within a 16-lane group the read hands lane j the four
+    // keys kb .. kb+3 of dim d0 + j
+    int vt_off[DBLK];
+    {
+        const int i = lane & 15;
+        const int rr = 4 * hh + (i >> 2);
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+            const int dim = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
+            vt_off[db] = rr * L::ROW + 16 * wv_slot<HD>(rr, dim >> 3) + 8 * ((dim >> 2) & 1);
+        }
+    }
+
+    // ---- online-softmax state per row block: running max m_used (log2 units of the
+    // pre-scaled score), its negated splat (seed of every S^T accumulator), `seen` (the row
+    // has had a visible key) and this lane's share of the row sum
+    f32x16 o[NB][DBLK];
+    f32x16 negm[NB];
+    float m_used[NB], l_part[NB];
+    bool seen[NB];
+#pragma unroll
+    for (int rb = 0; rb < NB; ++rb) {
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[rb][db][v] = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) negm[rb][v] = 0.f;
+        m_used[rb] = 0.f;
+        l_part[rb] = 0.f;
+        seen[rb] = false;
+    }
+    const f16x2 ones = {(_Float16)1.f, (_Float16)1.f};
+
+    // S^T tiles, double buffered: the step that exponentiates one computes the next tile's
+    // into the other (the two swap roles from step to step, so no copies)
+    typedef f32x16 STile[NB][SB];
+    STile sA, sB;
+
+    auto k_tile = [&](int par) { return (const lds_u8*)(lds3 + (par * KS + kg) * L::TILE); };
+    auto v_tile = [&](int par) { return (const lds_u8*)(lds3 + L::VBASE + (par * KS + kg) * L::TILE); };
+
+    // S^T of one tile, not interleaved (prologue)
+    auto s_tile = [&](STile& sn, const lds_u8* kl) {
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+            for (int sb = 0; sb < SB; ++sb) {
+                const f16x8 ka = *(const f16x8 __attribute__((address_space(3)))*)(kl + 32 * sb * L::ROW + ka_off[ks]);
+#pragma unroll
+                for (int rb = 0; rb < NB; ++rb) sn[rb][sb] = mfma32x32x16(ka, qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+            }
+    };
+    // causal / cache-end mask of tile t; wave-uniform test (diagonal and last tiles)
+    auto tile_needs_mask = [&](int t) { return t * BN + BN - 1 > a.q_base + w_first || t * BN + BN > a.n_ctx; };
+    auto mask_tile = [&](STile& sv, int t) {
+        const int key0 = t * BN;
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+            for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int key = key0 + 32 * sb + 8 * (v >> 2) + 4 * hh + (v & 3);
+                    const bool vis = key <= qpos[rb] && key < a.n_ctx;
+                    sv[rb][sb][v] = vis ? sv[rb][sb][v] : -INFINITY;
+                }
+    };
+    auto row_max = [&](const STile& sv, int rb) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int v = 0; v < 16; v += 2) m = __builtin_fmaxf(m, __builtin_fmaxf(sv[rb][sb][v], sv[rb][sb][v + 1]));
+        return max_xor32(m);
+    };
+    // lazy rescale: a row moves its max when it first sees a key, or when its scores exceed
+    // the current max by more than 2^8
+    auto rescale = [&](STile& sv, const float (&mx)[NB]) {
+        bool need[NB];
+        bool any_need = false;
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb) {
+            need[rb] = seen[rb] ? (mx[rb] > kRescaleThresh) : (mx[rb] > -INFINITY);
+            any_need = any_need || need[rb];
+        }
+        if (__any(any_need)) {
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) {
+                const float d = need[rb] ? mx[rb] : 0.f;
+                const float corr = fast_exp2(-d);
+                m_used[rb] += d;
+                seen[rb] = seen[rb] || need[rb];
+                l_part[rb] *= corr;
+#pragma unroll
+                for (int db = 0; db < DBLK; ++db) o[rb][db] *= corr;
+#pragma unroll
+                for (int sb = 0; sb < SB; ++sb) sv[rb][sb] -= d;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) negm[rb][v] = -m_used[rb];
+            }
+        }
+    };
+    // finish tile t's scores: mask if needed, row max, rescale
+    auto finish_scores = [&](STile& sv, int t, float (&mx)[NB]) {
+        if (tile_needs_mask(t)) {
+            mask_tile(sv, t);
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) mx[rb] = row_max(sv, rb);
+        }
+        rescale(sv, mx);
+    };
+    // P(t) in packed f16 pairs: pw[rb][sb][j][w] holds the B-operand dword w of keys
+    // 8 j + 2 w .. +1 of S^T block sb (register v = 8 j + 2 w of the accumulator)
+    typedef uint32_t PTile[NB][SB][2][4];
+    // probabilities of flattened score elements e, e + 1 (e = (rb * SB + sb) * 16 + v): exp2,
+    // f16 pack, row sum from the packed values (exactly what the PV MFMA consumes)
+    auto p_pair = [&](const STile& sc, PTile& pw, int e) {
+        const int rb = e / (SB * 16), sb = (e / 16) % SB, v = e % 16;
+        const f32x2 x = {fast_exp2(sc[rb][sb][v]), fast_exp2(sc[rb][sb][v + 1])};
+        const f16x2 h2 = __builtin_convertvector(x, f16x2);
+        pw[rb][sb][v / 8][(v % 8) / 2] = __builtin_bit_cast(uint32_t, h2);
+        l_part[rb] = __builtin_amdgcn_fdot2(h2, ones, l_part[rb], false);
+    };
+    auto p_operand = [&](const PTile& pw, int rb, int sb, int j) {
+        return __builtin_bit_cast(f16x8, u32x4{pw[rb][sb][j][0], pw[rb][sb][j][1], pw[rb][sb][j][2], pw[rb][sb][j][3]});
+    };
+    constexpr int KITER = KSTEPS * SB;                   // K operand reads per tile
+    constexpr int PELEMS = NB * SB * 16;                 // score elements per lane per tile
+    static_assert(PELEMS % (2 * KITER) == 0, "P pairs per K step");
+
+    // Phase A of a step: S^T(next) = K Q^T - m on the MFMAs, with P(t) on the VALU.  The
+    // program order below is the issue order (sched_barrier between slices): K reads run
+    // four operands ahead, each MFMA slot carries 1/KITER of the P work.
+    auto phase_a = [&](const lds_u8* kl, const STile& sc, STile& sn, PTile& pw) {
+        constexpr int AHEAD = KITER < 4 ? KITER : 4;
+        f16x8 ka[KITER];
+        auto rd = [&](auto I) {
+            constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
+            ka[i] = *(const f16x8 __attribute__((address_space(3)))*)(kl + 32 * sb * L::ROW + ka_off[ks]);
+        };
+        static_for<0, AHEAD>(rd);
+        static_for<0, KITER>([&](auto I) {
+            constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
+            if constexpr (i + AHEAD < KITER) rd(std::integral_constant<int, i + AHEAD>{});
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) sn[rb][sb] = mfma32x32x16(ka[i], qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+            constexpr int E = PELEMS / KITER;
+#pragma unroll
+            for (int e = i * E; e < (i + 1) * E; e += 2) p_pair(sc, pw, e);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    // O^T += V^T P^T over one tile, operand group gv = (sb, j, db); two groups of V^T reads in
+    // flight ahead of the MFMAs; between(gv) is VALU work issued behind group gv's MFMAs
+    constexpr int VGROUPS = SB * 2 * DBLK;
+    auto pv_tile = [&](const lds_u8* vl, const PTile& pw, auto between) {
+        u32x2 vr[VGROUPS][2];
+        auto rd = [&](auto GV) {
+            constexpr int gv = decltype(GV)::value;
+            constexpr int sb = gv / (2 * DBLK), j = (gv / DBLK) % 2, db = gv % DBLK;
+            vr[gv][0] = ds_read_tr16<(32 * sb + 16 * j) * L::ROW>(vl + vt_off[db]);
+            vr[gv][1] = ds_read_tr16<(32 * sb + 16 * j + 8) * L::ROW>(vl + vt_off[db]);
+        };
+        rd(std::integral_constant<int, 0>{});
+        rd(std::integral_constant<int, 1>{});
+        static_for<0, VGROUPS>([&](auto GV) {
+            constexpr int gv = decltype(GV)::value;
+            constexpr int sb = gv / (2 * DBLK), j = (gv / DBLK) % 2, db = gv % DBLK;
+            if constexpr (gv + 2 < VGROUPS) {
+                rd(std::integral_constant<int, gv + 2>{});
+                wait_lgkm<4>(vr[gv][0], vr[gv][1]);
+            } else if constexpr (gv + 1 < VGROUPS) {
+                wait_lgkm<2>(vr[gv][0], vr[gv][1]);
+            } else {
+                wait_lgkm<0>(vr[gv][0], vr[gv][1]);
+            }
+            const f16x8 va = __builtin_bit_cast(f16x8, u32x4{vr[gv][0][0], vr[gv][0][1], vr[gv][1][0], vr[gv][1][1]});
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) o[rb][db] = mfma32x32x16(va, p_operand(pw, rb, sb, j), o[rb][db]);
+            between(GV);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    // sync point of step s: this step's tiles landed, older slots free; the next loads go out
+    auto step_sync = [&](int s) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);                // this thread's tiles of the step landed
+        __syncthreads();                                     // ... every thread's; old slots free
+        if (s + 2 < n_steps) issue(s + 2, true);
+        if (s + 1 < n_steps) issue(s + 1, false);
+    };
+    // one full step: P(t) from sc, O += V(t)^T P(t)^T; S(t + KS) into sn, t = s KS + kg
+    auto step_full = [&](int s, auto PAR, STile& sc, STile& sn) {
+        constexpr int par = decltype(PAR)::value;
+        step_sync(s);
+        const int tn = (s + 1) * KS + kg;
+        PTile pw;
+        // phase A: S(tn) MFMAs, P(t) on the VALU
+        phase_a(k_tile(par ^ 1), sc, sn, pw);
+        // phase B: PV(t) MFMAs, row max of S(tn) on the VALU (running max3 over element pairs)
+        float mrun[NB];
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb) mrun[rb] = -INFINITY;
+        pv_tile(v_tile(par), pw, [&](auto GV) {
+            constexpr int gv = decltype(GV)::value;
+            constexpr int M = PELEMS / VGROUPS;
+#pragma unroll
+            for (int e = gv * M; e < (gv + 1) * M; e += 2) {
+                const int rb = e / (SB * 16), sb = (e / 16) % SB, v = e % 16;
+                mrun[rb] = __builtin_fmaxf(mrun[rb], __builtin_fmaxf(sn[rb][sb][v], sn[rb][sb][v + 1]));
+            }
+        });
+        float mx[NB];
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb) mx[rb] = max_xor32(mrun[rb]);
+        finish_scores(sn, tn, mx);
+    };
+    // the last step: P(t) and O += V(t)^T P(t)^T only (slot parity known at run time)
+    auto step_last = [&](int s, STile& sc) {
+        step_sync(s);
+        PTile pw;
+#pragma unroll
+        for (int e = 0; e < PELEMS; e += 2) p_pair(sc, pw, e);
+        pv_tile(lds3 + L::VBASE + ((s & 1) * KS + kg) * L::TILE, pw, [](auto) {});
+    };
+
+    // ---- prologue: first tiles resident, S of this wave's first tile
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    {
+        s_tile(sA, k_tile(0));
+        float mx[NB];
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb) mx[rb] = row_max(sA, rb);
+        finish_scores(sA, kg, mx);
+    }
+    // ---- key loop: n_steps - 1 full steps, two per iteration (S buffers swap roles), then
+    // the last step
+    int s = 0;
+    for (; s + 2 < n_steps; s += 2) {
+        step_full(s, std::integral_constant<int, 0>{}, sA, sB);
+        step_full(s + 1, std::integral_constant<int, 1>{}, sB, sA);
+    }
+    if (s + 1 < n_steps) {
+        step_full(s, std::integral_constant<int, 0>{}, sA, sB);
+        step_last(s + 1, sB);
+    } else {
+        step_last(s, sA);
+    }
+
+    // ---- epilogue
+    float l_tot[NB];
+#pragma unroll
+    for (int rb = 0; rb < NB; ++rb) l_tot[rb] = sum_xor32(l_part[rb]);
+
+    if constexpr (KS > 1) {
+        // key group 1 hands (O, m, l) to key group 0 through LDS; lane-major, conflict free
+        __syncthreads();                                     // ring reads done
+        float* mrg = (float*)lds + rw * L::MERGE_FLOATS;
+        if (kg == 1) {
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) {
+#pragma unroll
+                for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) mrg[((rb * DBLK + db) * 16 + v) * 64 + lane] = o[rb][db][v];
+                mrg[NB * DBLK * 16 * 64 + (2 * rb) * 64 + lane] = seen[rb] ? m_used[rb] : -INFINITY;
+                mrg[NB * DBLK * 16 * 64 + (2 * rb + 1) * 64 + lane] = l_tot[rb];
+            }
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) {
+                const float m1 = mrg[NB * DBLK * 16 * 64 + (2 * rb) * 64 + lane];
+                const float l1 = mrg[NB * DBLK * 16 * 64 + (2 * rb + 1) * 64 + lane];
+                const float m0 = seen[rb] ? m_used[rb] : -INFINITY;
+                const float mn = fmaxf(m0, m1);
+                const float c0 = mn == -INFINITY ? 0.f : fast_exp2(m0 - mn);
+                const float c1 = mn == -INFINITY ? 0.f : fast_exp2(m1 - mn);
+                l_tot[rb] = l_tot[rb] * c0 + l1 * c1;
+#pragma unroll
+                for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        o[rb][db][v] = o[rb][db][v] * c0 + mrg[((rb * DBLK + db) * 16 + v) * 64 + lane] * c1;
+            }
+        }
+    }
+    if (kg != 0 || !wave_active) return;
+
+    // lane (row n, hh) holds dims 32 db + 8 a4 + 4 hh + (0..3) of its row
+#pragma unroll
+    for (int rb = 0; rb < NB; ++rb) {
+        const int qrow = w_first + 32 * rb + n;
+        if (qrow >= a.n_query) continue;
+        const float inv = l_tot[rb] > 0.f ? 1.f / l_tot[rb] : 0.f;
+        const size_t obase = ((size_t)qrow * a.n_q_heads + h) * HD;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                const int dim = 32 * db + 8 * a4 + 4 * hh;
+                const float v0 = o[rb][db][4 * a4] * inv, v1 = o[rb][db][4 * a4 + 1] * inv;
+                const float v2 = o[rb][db][4 * a4 + 2] * inv, v3 = o[rb][db][4 * a4 + 3] * inv;
+                if constexpr (O_F32) {
+                    *(f32x4*)((float*)a.out + obase + dim) = f32x4{v0, v1, v2, v3};
+                } else {
+                    f32x2 p0 = {v0, v1}, p1 = {v2, v3};
+                    f16x2 h0 = __builtin_convertvector(p0, f16x2);
+                    f16x2 h1 = __builtin_convertvector(p1, f16x2);
+                    *(u32x2*)((uint16_t*)a.out + obase + dim) =
+                        u32x2{__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
+                }
+            }
+    }
+}
+
+// ---- launchers
+
+int prefill_wide_rows(int ks) { return (4 / ks) * kWideRowsPerWave; }
+
+template <int HD, int KS, bool QF, bool OF>
+static hipError_t launch_wide_t(const PrefillArgs& a, hipStream_t stream)
+{
+    constexpr int lds_bytes = WideLayout<HD, KS>::LDS_BYTES;
+    static bool attr_done = false;        // set once per instantiation (benign race: idempotent)
+    if (!attr_done) {
+        hipError_t e = hipFuncSetAttribute((const void*)prefill_wide_kernel<HD, KS, QF, OF>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    hipLaunchKernelGGL((prefill_wide_kernel<HD, KS, QF, OF>), dim3(a.n_items), dim3(kPrefillThreads),
+                       lds_bytes, stream, a);
+    return hipGetLastError();
+}
+
+template <int HD, int KS>
+static hipError_t launch_wide_ks(const PrefillArgs& a, bool q_f32, bool o_f32, hipStream_t s)
+{
+    if (q_f32) return o_f32 ? launch_wide_t<HD, KS, true, true>(a, s) : launch_wide_t<HD, KS, true, false>(a, s);
+    return o_f32 ? launch_wide_t<HD, KS, false, true>(a, s) : launch_wide_t<HD, KS, false, false>(a, s);
+}
+
+bool prefill_wide_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
+
+hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32,
+                               hipStream_t stream)
+{
+    if (ks != 1 && ks != 2) return hipErrorInvalidValue;
+    switch (head_dim) {
+    case 64: return ks == 1 ? launch_wide_ks<64, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<64, 2>(a, q_f32, o_f32, stream);
+    case 128: return ks == 1 ? launch_wide_ks<128, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<128, 2>(a, q_f32, o_f32, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace nxa

@@ -62,6 +62,11 @@ PREFILL_CASES = [
     (8, 4, 128, 100, 60, 0, False, False, 0, 30.0),    # softcap
     (8, 2, 128, 64, 2000, 0, True, True, 0, 0.0),      # long cache, short chunk (split path)
     (40, 8, 128, 33, 1000, 0, True, True, 0, 0.0),     # cfg-2 head layout, small
+    # pipelined kernel with 128-row blocks (>= one block per CU of a 256-CU MI355X)
+    (64, 8, 128, 520, 37, 3, False, False, 0, 0.0),    # ragged last block, unaligned base, f32 q/o
+    (64, 16, 64, 512, 0, 0, True, True, 0, 0.0),       # hd 64
+    # pipelined kernel, 64-row blocks, odd tile count: key group 1 runs one tile past the end
+    (8, 2, 128, 80, 0, 0, True, False, 0, 0.0),
 ]
 
 
@@ -92,11 +97,14 @@ def test_prefill_golden(hip, golden):
     assert_close(got, golden["pre_a_out"], "golden pre_a")
 
 
-def test_prefill_split_equals_unsplit(hip):
+@pytest.mark.parametrize("cap", [0.0, 30.0])
+def test_prefill_split_equals_unsplit(hip, cap):
+    """With a workspace the kernel may split the key range (the softcap shape takes the split
+    path of prefill_kernel); the result must not depend on it."""
     hq, hkv, hd, nq, base = 8, 2, 128, 256, 3000
     q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=4, q_f16=True)
-    a = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, split=True)
-    b = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, split=False)
+    a = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, cap=cap, split=True)
+    b = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, cap=cap, split=False)
     assert O.max_abs(a, b) < 1e-3 and O.rel_l2(a, b) < 5e-4
 
 
