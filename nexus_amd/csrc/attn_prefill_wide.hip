@@ -5,7 +5,8 @@
 // (src/model/transformer.h:8653-8685) and attn_flash.comp (src/gpu/shaders/attn_flash.comp:
 // 66-72, 121-159): query i sits at absolute position q_base + i and sees keys
 // [0, min(q_base + i, n_ctx - 1)].  This kernel takes the plain causal shapes (no logit
-// softcap, no sliding window, no key split across workgroups); prefill_kernel keeps those.
+// softcap, no sliding window); prefill_kernel keeps those.  A key split across workgroups
+// writes the reference's split-K partials for the combine kernel, as prefill_kernel does.
 //
 // Design:
 //  * A wave owns 32 query rows; two waves per SIMD.  Workgroup = 4 waves.  KS = 1: four row
@@ -20,12 +21,13 @@
 //    two S^T tiles swap roles from step to step (loop unrolled by two, no copies).
 //  * Every wave of a workgroup runs the same steps: no per-wave branch in the loop body, so
 //    O, Q^T and both S^T tiles keep fixed registers (the last step is peeled).
-//  * K runs one tile ahead of V in the LDS ring: during step s the ring holds K(s+1) and V(s)
-//    and receives K(s+2) and V(s+1) (buffer-load-to-LDS of XOR-swizzled 16-byte chunks, the
-//    slot layout of prefill_kernel), one barrier per step.
+//  * K runs one tile ahead of V in an LDS ring of two tiles per operand: step s reads K(s+1)
+//    and V(s) while K(s+2) and V(s+1) load (buffer-load-to-LDS of XOR-swizzled 16-byte chunks,
+//    the slot layout of prefill_kernel); one barrier per step.  With the loop unrolled by two
+//    the slot parity is static, so every LDS address is a per-lane register plus an immediate.
 //  * S^T = K Q^T with Q pre-scaled by scale * log2(e) and the accumulator seeded with -m, so a
 //    probability is one exp2; the running max moves lazily (only past a 2^8 margin), the row
-//    max is v_max3 + v_permlane32_swap, row sums are v_dot2 over the packed f16 P.
+//    max is v_max3 + v_permlane32_swap, row sums are fp32 adds of the probabilities.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -47,7 +49,10 @@ struct WideLayout {
     static constexpr int ROW = HD * 2;                          // bytes per K/V row
     static constexpr int CPR = HD / 8;                          // 16-byte chunks per row
     static constexpr int TILE = BN * ROW;
-    static constexpr int SLOTS = 2 * KS;                        // ring slots per operand
+    // K and V each hold two tiles per key group: the step being computed and the next one
+    // (loading); with the loop unrolled by two, every LDS address is an immediate offset
+    static constexpr int DEPTH = 2;
+    static constexpr int SLOTS = DEPTH * KS;                    // ring slots per operand
     static constexpr int VBASE = SLOTS * TILE;
     static constexpr int RING_BYTES = 2 * SLOTS * TILE;
     // KS = 2: per row wave, O of both row blocks (16 registers x 64 lanes per 32-dim block)
@@ -82,11 +87,24 @@ __device__ __forceinline__ u32x2 ds_read_tr16(const lds_u8* p)
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF) : "memory");
     return r;
 }
-// s_waitcnt lgkmcnt(N), ordered before every use of the two registers
+// ds_read_b128 as inline asm, for the same reason (K operands); waited for with wait_lgkm
+template <int OFF>
+__device__ __forceinline__ u32x4 ds_read_b128(const lds_u8* p)
+{
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF) : "memory");
+    return r;
+}
+// s_waitcnt lgkmcnt(N), ordered before every use of the registers
 template <int N>
 __device__ __forceinline__ void wait_lgkm(u32x2& a, u32x2& b)
 {
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm(u32x4& a)
+{
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
 }
 
 // f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
@@ -99,8 +117,13 @@ __device__ __forceinline__ void static_for(F&& f)
     }
 }
 
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
-constexpr int kWaitVm0 = 0x0f70;
+// operand read-ahead: V^T operand groups in flight ahead of the PV MFMAs, K operands ahead of
+// the S MFMAs
+constexpr int kWideVAhead = 2;
+constexpr int kWideKAhead = 4;
+
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt left at their maxima)
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
 
 }  // namespace
 
@@ -119,24 +142,32 @@ prefill_wide_kernel(PrefillArgs a)
     const int n = lane & 31, hh = lane >> 5;
     const int rw = wave % L::RWAVES, kg = wave / L::RWAVES;
 
-    // ---- work item: (kv head, query block [heaviest first], q head in group)
+    // ---- work item: (kv head, query block [heaviest first], q head in group, key split)
     const int item = xcd_remap(blockIdx.x, a.n_items);
-    const int per_kv = a.group * a.n_qblocks;
+    const int per_kv = a.group * a.n_qblocks * a.n_splits;
     const int kvh = item / per_kv;
-    const int r = item - kvh * per_kv;
-    const int qb = a.n_qblocks - 1 - r / a.group;
-    const int g = r - (r / a.group) * a.group;
+    int r = item - kvh * per_kv;
+    const int qb = a.n_qblocks - 1 - r / (a.group * a.n_splits);
+    r %= a.group * a.n_splits;
+    const int g = r / a.n_splits;
+    const int split = r - g * a.n_splits;
     const int h = kvh * a.group + g;
 
+    // ---- key tiles of this workgroup: [t0, t1) of the block's tiles 0 .. k_hi / BN, split
+    // evenly over n_splits workgroups; keys from kmax on belong to later splits (or past the
+    // cache end) and are masked
     const int q0 = qb * BM;
     const int k_hi = min(a.q_base + min(q0 + BM, a.n_query) - 1, a.n_ctx - 1);
-    const int t_end = k_hi / BN + 1;                     // the workgroup's tiles: 0 .. t_end - 1
-    const int n_steps = (t_end + KS - 1) / KS;
+    const int n_tiles = k_hi / BN + 1;
+    const int tps = (n_tiles + a.n_splits - 1) / a.n_splits;
+    const int t0 = min(split * tps, n_tiles), t1 = min(t0 + tps, n_tiles);
+    const int kmax = min(a.n_ctx, t1 * BN);
+    const int n_steps = (t1 - t0 + KS - 1) / KS;         // 0 for an empty split
 
     // ---- this wave's rows.  Every wave runs all n_steps steps of the workgroup (same trip
     // count, no per-wave branches in the loop): tiles past a wave's diagonal are fully masked
-    // for it, and key group 1 of an odd tile count takes one tile past the last (loaded like
-    // any other, zero past the cache end, fully masked by causality).
+    // for it, and key group 1 of an odd tile count takes one tile past t1 (loaded like any
+    // other, zero past the cache end, fully masked).
     const int w_first = q0 + RPW * rw;
     const bool wave_active = w_first < a.n_query;
     int qpos[NB];
@@ -158,32 +189,39 @@ prefill_wide_kernel(PrefillArgs a)
         koff = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row, slot));
         voff = (uint32_t)(row * L::ROW + 16 * wv_slot<HD>(row, slot));
     }
-    // tiles of step `st`: tile st * KS + i goes to slot (st & 1) * KS + i
-    auto issue = [&](int st, bool k_side) {
+    // tiles of step `st`: tile st * KS + i goes to slot (st % 2) * KS + i.  Loads past the cache
+    // end are issued too (the descriptor returns zeros): every step issues the same number of
+    // loads, so a fixed vmcnt tells when a step's tiles have landed.
+    constexpr int D = L::DEPTH;
+    constexpr int LPS = 2 * L::LOADS * KS;                 // loads per thread per step (K + V)
+    static_assert((D - 1) * LPS <= 63, "vmcnt range");
+    auto issue_tiles = [&](int st, bool k_side) {
+        const int slot0 = (st & 1) * KS;
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
-            const int t = st * KS + i;
-            {
-                const int base = t * BN * L::ROW;
-                lds_u8* dst = lds3 + (k_side ? 0 : L::VBASE) + ((st & 1) * KS + i) * L::TILE + 1024 * wave;
+            const int base = (t0 + st * KS + i) * BN * L::ROW;
+            lds_u8* dst = lds3 + (k_side ? 0 : L::VBASE) + (slot0 + i) * L::TILE + 1024 * wave;
 #pragma unroll
-                for (int j = 0; j < L::LOADS; ++j)
-                    // the whole offset in the vector operand: the descriptor's range check
-                    // (zeros past the cache end) covers it
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        k_side ? krs : vrs, (void __attribute__((address_space(3)))*)(dst + 4096 * j), 16,
-                        (int)(k_side ? koff : voff) + base + 4096 * j, 0, 0, 0);
-            }
+            for (int j = 0; j < L::LOADS; ++j)
+                // the whole offset in the vector operand: the descriptor's range check
+                // (zeros past the cache end) covers it
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    k_side ? krs : vrs, (void __attribute__((address_space(3)))*)(dst + 4096 * j), 16,
+                    (int)(k_side ? koff : voff) + base + 4096 * j, 0, 0, 0);
         }
     };
-    issue(0, true);
-    issue(0, false);
-    if (n_steps > 1) issue(1, true);
+    // group st: what step st consumes, K(st + 1) and V(st)
+    auto issue_group = [&](int st) {
+        issue_tiles(st + 1, true);
+        issue_tiles(st, false);
+    };
 
     // ---- Q^T operands of both row blocks, pre-scaled by scale * log2(e): lane (row n, k-group
-    // hh) holds dims 16 ks + 8 hh .. +7
+    // hh) holds dims 16 ks + 8 hh .. +7.  The raw loads go out first, then the ring prologue,
+    // then the conversion (which waits for the Q loads only).
     constexpr uint32_t QE = Q_F32 ? 4u : 2u;
-    f16x8 qt[NB][KSTEPS];
+    constexpr int QV = Q_F32 ? 2 : 1;                      // 16-byte loads per k-step
+    u32x4 qraw[NB][KSTEPS][QV];
     {
         const size_t row_bytes = (size_t)a.n_q_heads * HD * QE;
         const int blk_rows = min(BM, a.n_query - q0);
@@ -192,33 +230,51 @@ prefill_wide_kernel(PrefillArgs a)
         for (int rb = 0; rb < NB; ++rb) {
             const uint32_t qoff = (uint32_t)((RPW * rw + 32 * rb + n) * row_bytes + ((size_t)h * HD + 8 * hh) * QE);
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-                float x[8];
-                if constexpr (Q_F32) {
-                    const f32x4 x0 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks));
-                    const f32x4 x1 = __builtin_bit_cast(f32x4, buf_load16(qr, qoff + 64 * ks + 16));
+            for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        x[i] = x0[i];
-                        x[4 + i] = x1[i];
-                    }
-                } else {
-                    const f16x8 hq = as_f16x8(buf_load16(qr, qoff + 32 * ks));
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) x[i] = (float)hq[i];
-                }
-                const float qs = a.scale_log2;
-                qt[rb][ks] = cvt_f16x8(x[0] * qs, x[1] * qs, x[2] * qs, x[3] * qs, x[4] * qs, x[5] * qs,
-                                       x[6] * qs, x[7] * qs);
-            }
+                for (int u = 0; u < QV; ++u) qraw[rb][ks][u] = buf_load16(qr, qoff + 16 * QE * ks + 16 * u);
         }
     }
+
+    // ring prologue: K(0), then the groups of steps 0 .. D - 2 (kept behind the Q loads, so
+    // converting Q waits for Q only)
+    __builtin_amdgcn_sched_barrier(0);
+    if (n_steps > 0) {
+        issue_tiles(0, true);
+#pragma unroll
+        for (int st = 0; st < D - 1; ++st) issue_group(st);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    f16x8 qt[NB][KSTEPS];
+#pragma unroll
+    for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            float x[8];
+            if constexpr (Q_F32) {
+                const f32x4 x0 = __builtin_bit_cast(f32x4, qraw[rb][ks][0]);
+                const f32x4 x1 = __builtin_bit_cast(f32x4, qraw[rb][ks][QV - 1]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x[i] = x0[i];
+                    x[4 + i] = x1[i];
+                }
+            } else {
+                const f16x8 hq = as_f16x8(qraw[rb][ks][0]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = (float)hq[i];
+            }
+            const float qs = a.scale_log2;
+            qt[rb][ks] = cvt_f16x8(x[0] * qs, x[1] * qs, x[2] * qs, x[3] * qs, x[4] * qs, x[5] * qs,
+                                   x[6] * qs, x[7] * qs);
+        }
 
     // ---- per-lane LDS read offsets within a tile
     // K operand of block sb, k-step ks: row 32 sb + n, chunk 2 ks + hh
     int ka_off[KSTEPS];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) ka_off[ks] = n * L::ROW + 16 * wk_slot<HD>(n, 2 * ks + hh);
+    for (int ks = 0; ks < KSTEPS; ++ks) ka_off[ks] = kg * L::TILE + n * L::ROW + 16 * wk_slot<HD>(n, 2 * ks + hh);
     // V^T transposing reads: source lane i = lane & 15 of each 16-lane group addresses
     // V[kb + i/4][d0 + 4 (i%4)], kb = 32 sb + 16 j + 4 hh (+8 for the second read),
     // d0 = 32 db + 16 ((lane >> 4) & 1); within a 16-lane group the read hands lane j the four
@@ -230,7 +286,7 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
         for (int db = 0; db < DBLK; ++db) {
             const int dim = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
-            vt_off[db] = rr * L::ROW + 16 * wv_slot<HD>(rr, dim >> 3) + 8 * ((dim >> 2) & 1);
+            vt_off[db] = L::VBASE + kg * L::TILE + rr * L::ROW + 16 * wv_slot<HD>(rr, dim >> 3) + 8 * ((dim >> 2) & 1);
         }
     }
 
@@ -253,29 +309,30 @@ prefill_wide_kernel(PrefillArgs a)
         l_part[rb] = 0.f;
         seen[rb] = false;
     }
-    const f16x2 ones = {(_Float16)1.f, (_Float16)1.f};
 
     // S^T tiles, double buffered: the step that exponentiates one computes the next tile's
     // into the other (the two swap roles from step to step, so no copies)
     typedef f32x16 STile[NB][SB];
     STile sA, sB;
+    constexpr bool kSCopy = NB > 1;
 
-    auto k_tile = [&](int par) { return (const lds_u8*)(lds3 + (par * KS + kg) * L::TILE); };
-    auto v_tile = [&](int par) { return (const lds_u8*)(lds3 + L::VBASE + (par * KS + kg) * L::TILE); };
+    // byte offset of ring slot parity `par` (key group 0) for K or V; the key group's slot
+    // offset is folded into ka_off / vt_off
+    constexpr int SLOT_PAR = KS * L::TILE;
 
     // S^T of one tile, not interleaved (prologue)
-    auto s_tile = [&](STile& sn, const lds_u8* kl) {
+    auto s_tile = [&](STile& sn) {
+        static_for<0, KSTEPS * SB>([&](auto I) {
+            constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
+            u32x4 ka = ds_read_b128<32 * sb * L::ROW>(lds3 + ka_off[ks]);
+            wait_lgkm<0>(ka);
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-#pragma unroll
-            for (int sb = 0; sb < SB; ++sb) {
-                const f16x8 ka = *(const f16x8 __attribute__((address_space(3)))*)(kl + 32 * sb * L::ROW + ka_off[ks]);
-#pragma unroll
-                for (int rb = 0; rb < NB; ++rb) sn[rb][sb] = mfma32x32x16(ka, qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
-            }
+            for (int rb = 0; rb < NB; ++rb)
+                sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+        });
     };
     // causal / cache-end mask of tile t; wave-uniform test (diagonal and last tiles)
-    auto tile_needs_mask = [&](int t) { return t * BN + BN - 1 > a.q_base + w_first || t * BN + BN > a.n_ctx; };
+    auto tile_needs_mask = [&](int t) { return t * BN + BN - 1 > a.q_base + w_first || t * BN + BN > kmax; };
     auto mask_tile = [&](STile& sv, int t) {
         const int key0 = t * BN;
 #pragma unroll
@@ -285,7 +342,7 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int key = key0 + 32 * sb + 8 * (v >> 2) + 4 * hh + (v & 3);
-                    const bool vis = key <= qpos[rb] && key < a.n_ctx;
+                    const bool vis = key <= qpos[rb] && key < kmax;
                     sv[rb][sb][v] = vis ? sv[rb][sb][v] : -INFINITY;
                 }
     };
@@ -337,13 +394,14 @@ prefill_wide_kernel(PrefillArgs a)
     // 8 j + 2 w .. +1 of S^T block sb (register v = 8 j + 2 w of the accumulator)
     typedef uint32_t PTile[NB][SB][2][4];
     // probabilities of flattened score elements e, e + 1 (e = (rb * SB + sb) * 16 + v): exp2,
-    // f16 pack, row sum from the packed values (exactly what the PV MFMA consumes)
+    // f16 pack, fp32 row sum.  (The sum uses fp32 adds, not v_dot2 on the packed pair: on
+    // gfx950 v_dot2 does not issue alongside the MFMAs, the adds do.)
     auto p_pair = [&](const STile& sc, PTile& pw, int e) {
         const int rb = e / (SB * 16), sb = (e / 16) % SB, v = e % 16;
         const f32x2 x = {fast_exp2(sc[rb][sb][v]), fast_exp2(sc[rb][sb][v + 1])};
         const f16x2 h2 = __builtin_convertvector(x, f16x2);
         pw[rb][sb][v / 8][(v % 8) / 2] = __builtin_bit_cast(uint32_t, h2);
-        l_part[rb] = __builtin_amdgcn_fdot2(h2, ones, l_part[rb], false);
+        l_part[rb] += x[0] + x[1];
     };
     auto p_operand = [&](const PTile& pw, int rb, int sb, int j) {
         return __builtin_bit_cast(f16x8, u32x4{pw[rb][sb][j][0], pw[rb][sb][j][1], pw[rb][sb][j][2], pw[rb][sb][j][3]});
@@ -354,20 +412,26 @@ prefill_wide_kernel(PrefillArgs a)
 
     // Phase A of a step: S^T(next) = K Q^T - m on the MFMAs, with P(t) on the VALU.  The
     // program order below is the issue order (sched_barrier between slices): K reads run
-    // four operands ahead, each MFMA slot carries 1/KITER of the P work.
-    auto phase_a = [&](const lds_u8* kl, const STile& sc, STile& sn, PTile& pw) {
-        constexpr int AHEAD = KITER < 4 ? KITER : 4;
-        f16x8 ka[KITER];
+    // four operands ahead (explicit lgkmcnt waits: the only LDS operations in flight are
+    // these reads), each MFMA slot carries 1/KITER of the P work.
+    auto phase_a = [&](auto KPAR, const STile& sc, STile& sn, PTile& pw) {
+        constexpr int kbase = decltype(KPAR)::value * SLOT_PAR;
+        constexpr int AHEAD = KITER < kWideKAhead ? KITER : kWideKAhead;
+        u32x4 ka[KITER];
         auto rd = [&](auto I) {
             constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
-            ka[i] = *(const f16x8 __attribute__((address_space(3)))*)(kl + 32 * sb * L::ROW + ka_off[ks]);
+            ka[i] = ds_read_b128<kbase + 32 * sb * L::ROW>(lds3 + ka_off[ks]);
         };
         static_for<0, AHEAD>(rd);
         static_for<0, KITER>([&](auto I) {
             constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
             if constexpr (i + AHEAD < KITER) rd(std::integral_constant<int, i + AHEAD>{});
+            // reads issued after read i: i + 1 .. min(i + AHEAD, KITER - 1)
+            constexpr int LATER = (KITER - 1 - i) < AHEAD ? (KITER - 1 - i) : AHEAD;
+            wait_lgkm<LATER>(ka[i]);
 #pragma unroll
-            for (int rb = 0; rb < NB; ++rb) sn[rb][sb] = mfma32x32x16(ka[i], qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+            for (int rb = 0; rb < NB; ++rb)
+                sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
             constexpr int E = PELEMS / KITER;
 #pragma unroll
             for (int e = i * E; e < (i + 1) * E; e += 2) p_pair(sc, pw, e);
@@ -378,27 +442,24 @@ prefill_wide_kernel(PrefillArgs a)
     // O^T += V^T P^T over one tile, operand group gv = (sb, j, db); two groups of V^T reads in
     // flight ahead of the MFMAs; between(gv) is VALU work issued behind group gv's MFMAs
     constexpr int VGROUPS = SB * 2 * DBLK;
-    auto pv_tile = [&](const lds_u8* vl, const PTile& pw, auto between) {
+    auto pv_tile = [&](auto VPAR, const PTile& pw, auto between) {
+        constexpr int vbase = decltype(VPAR)::value * SLOT_PAR;
+        constexpr int VAH = kWideVAhead < VGROUPS ? kWideVAhead : VGROUPS;   // groups in flight
         u32x2 vr[VGROUPS][2];
         auto rd = [&](auto GV) {
             constexpr int gv = decltype(GV)::value;
             constexpr int sb = gv / (2 * DBLK), j = (gv / DBLK) % 2, db = gv % DBLK;
-            vr[gv][0] = ds_read_tr16<(32 * sb + 16 * j) * L::ROW>(vl + vt_off[db]);
-            vr[gv][1] = ds_read_tr16<(32 * sb + 16 * j + 8) * L::ROW>(vl + vt_off[db]);
+            vr[gv][0] = ds_read_tr16<vbase + (32 * sb + 16 * j) * L::ROW>(lds3 + vt_off[db]);
+            vr[gv][1] = ds_read_tr16<vbase + (32 * sb + 16 * j + 8) * L::ROW>(lds3 + vt_off[db]);
         };
-        rd(std::integral_constant<int, 0>{});
-        rd(std::integral_constant<int, 1>{});
+        static_for<0, VAH>(rd);
         static_for<0, VGROUPS>([&](auto GV) {
             constexpr int gv = decltype(GV)::value;
             constexpr int sb = gv / (2 * DBLK), j = (gv / DBLK) % 2, db = gv % DBLK;
-            if constexpr (gv + 2 < VGROUPS) {
-                rd(std::integral_constant<int, gv + 2>{});
-                wait_lgkm<4>(vr[gv][0], vr[gv][1]);
-            } else if constexpr (gv + 1 < VGROUPS) {
-                wait_lgkm<2>(vr[gv][0], vr[gv][1]);
-            } else {
-                wait_lgkm<0>(vr[gv][0], vr[gv][1]);
-            }
+            if constexpr (gv + VAH < VGROUPS) rd(std::integral_constant<int, gv + VAH>{});
+            // reads issued after group gv's: groups gv + 1 .. min(gv + VAH, VGROUPS - 1)
+            constexpr int LATER = (VGROUPS - 1 - gv) < VAH ? (VGROUPS - 1 - gv) : VAH;
+            wait_lgkm<2 * LATER>(vr[gv][0], vr[gv][1]);
             const f16x8 va = __builtin_bit_cast(f16x8, u32x4{vr[gv][0][0], vr[gv][0][1], vr[gv][1][0], vr[gv][1][1]});
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) o[rb][db] = mfma32x32x16(va, p_operand(pw, rb, sb, j), o[rb][db]);
@@ -408,75 +469,114 @@ prefill_wide_kernel(PrefillArgs a)
     };
 
     // sync point of step s: this step's tiles landed, older slots free; the next loads go out
+    // The ring needs no memory fence: the loads land in LDS, each thread waits for its own
+    // (vmcnt) and every LDS read of the previous step has returned (lgkmcnt) before the
+    // barrier.  (A workgroup fence here makes the compiler drain every in-flight load.)
     auto step_sync = [&](int s) {
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);                // this thread's tiles of the step landed
-        __syncthreads();                                     // ... every thread's; old slots free
-        if (s + 2 < n_steps) issue(s + 2, true);
-        if (s + 1 < n_steps) issue(s + 1, false);
+        __builtin_amdgcn_s_waitcnt(wait_vm((D - 2) * LPS));  // this thread's group s landed
+        __builtin_amdgcn_s_barrier();                        // ... every thread's; step s-1 done
+        issue_group(s + D - 1);                              // into the slots step s-1 freed
     };
     // one full step: P(t) from sc, O += V(t)^T P(t)^T; S(t + KS) into sn, t = s KS + kg
+    // sc: S(t) (VALU side); sn: where the MFMAs put S(tn).  kSCopy: sn is a separate MFMA
+    // accumulator whose values are copied into sc during phase B (then sc holds S(tn) for the
+    // next step); otherwise sc and sn swap roles from step to step.
     auto step_full = [&](int s, auto PAR, STile& sc, STile& sn) {
-        constexpr int par = decltype(PAR)::value;
+        constexpr int par = decltype(PAR)::value;                 // s % 2
         step_sync(s);
-        const int tn = (s + 1) * KS + kg;
+        const int tn = t0 + (s + 1) * KS + kg;
         PTile pw;
         // phase A: S(tn) MFMAs, P(t) on the VALU
-        phase_a(k_tile(par ^ 1), sc, sn, pw);
+        phase_a(std::integral_constant<int, par ^ 1>{}, sc, sn, pw);
         // phase B: PV(t) MFMAs, row max of S(tn) on the VALU (running max3 over element pairs)
+        STile& sx = kSCopy ? sc : sn;
         float mrun[NB];
 #pragma unroll
         for (int rb = 0; rb < NB; ++rb) mrun[rb] = -INFINITY;
-        pv_tile(v_tile(par), pw, [&](auto GV) {
+        pv_tile(PAR, pw, [&](auto GV) {
             constexpr int gv = decltype(GV)::value;
             constexpr int M = PELEMS / VGROUPS;
 #pragma unroll
             for (int e = gv * M; e < (gv + 1) * M; e += 2) {
                 const int rb = e / (SB * 16), sb = (e / 16) % SB, v = e % 16;
-                mrun[rb] = __builtin_fmaxf(mrun[rb], __builtin_fmaxf(sn[rb][sb][v], sn[rb][sb][v + 1]));
+                if constexpr (kSCopy) {
+                    sc[rb][sb][v] = sn[rb][sb][v];
+                    sc[rb][sb][v + 1] = sn[rb][sb][v + 1];
+                }
+                mrun[rb] = __builtin_fmaxf(mrun[rb], __builtin_fmaxf(sx[rb][sb][v], sx[rb][sb][v + 1]));
             }
         });
         float mx[NB];
 #pragma unroll
         for (int rb = 0; rb < NB; ++rb) mx[rb] = max_xor32(mrun[rb]);
-        finish_scores(sn, tn, mx);
+        finish_scores(sx, tn, mx);
     };
-    // the last step: P(t) and O += V(t)^T P(t)^T only (slot parity known at run time)
-    auto step_last = [&](int s, STile& sc) {
+    // the last step: P(t) and O += V(t)^T P(t)^T only
+    auto step_last = [&](int s, auto PAR, STile& sc) {
         step_sync(s);
         PTile pw;
 #pragma unroll
         for (int e = 0; e < PELEMS; e += 2) p_pair(sc, pw, e);
-        pv_tile(lds3 + L::VBASE + ((s & 1) * KS + kg) * L::TILE, pw, [](auto) {});
+        pv_tile(PAR, pw, [](auto) {});
     };
 
-    // ---- prologue: first tiles resident, S of this wave's first tile
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __syncthreads();
-    {
-        s_tile(sA, k_tile(0));
-        float mx[NB];
+    if (n_steps > 0) {                                     // workgroup-uniform: empty split
+        // ---- prologue: K(0) resident, S of this wave's first tile
+        __builtin_amdgcn_s_waitcnt(wait_vm((D - 1) * LPS));
+        __builtin_amdgcn_s_barrier();
+        {
+            if constexpr (kSCopy) {
+                s_tile(sB);
 #pragma unroll
-        for (int rb = 0; rb < NB; ++rb) mx[rb] = row_max(sA, rb);
-        finish_scores(sA, kg, mx);
-    }
-    // ---- key loop: n_steps - 1 full steps, two per iteration (S buffers swap roles), then
-    // the last step
-    int s = 0;
-    for (; s + 2 < n_steps; s += 2) {
-        step_full(s, std::integral_constant<int, 0>{}, sA, sB);
-        step_full(s + 1, std::integral_constant<int, 1>{}, sB, sA);
-    }
-    if (s + 1 < n_steps) {
-        step_full(s, std::integral_constant<int, 0>{}, sA, sB);
-        step_last(s + 1, sB);
-    } else {
-        step_last(s, sA);
+                for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+                    for (int sb = 0; sb < SB; ++sb) sA[rb][sb] = sB[rb][sb];
+            } else {
+                s_tile(sA);
+            }
+            float mx[NB];
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) mx[rb] = row_max(sA, rb);
+            finish_scores(sA, t0 + kg, mx);
+        }
+        // ---- key loop: n_steps - 1 full steps, two per iteration (S buffers swap roles), then
+        // the last step
+        int s = 0;
+        if constexpr (kSCopy) {
+            for (; s + 2 < n_steps; s += 2) {
+                step_full(s, std::integral_constant<int, 0>{}, sA, sB);
+                step_full(s + 1, std::integral_constant<int, 1>{}, sA, sB);
+            }
+            if (s + 1 < n_steps) {
+                step_full(s, std::integral_constant<int, 0>{}, sA, sB);
+                step_last(s + 1, std::integral_constant<int, 1>{}, sA);
+            } else {
+                step_last(s, std::integral_constant<int, 0>{}, sA);
+            }
+        } else {
+            for (; s + 2 < n_steps; s += 2) {
+                step_full(s, std::integral_constant<int, 0>{}, sA, sB);
+                step_full(s + 1, std::integral_constant<int, 1>{}, sB, sA);
+            }
+            if (s + 1 < n_steps) {
+                step_full(s, std::integral_constant<int, 0>{}, sA, sB);
+                step_last(s + 1, std::integral_constant<int, 1>{}, sB);
+            } else {
+                step_last(s, std::integral_constant<int, 0>{}, sA);
+            }
+        }
     }
 
+    // the loads past the end are still in flight: none may land in LDS after this point
+    __builtin_amdgcn_s_waitcnt(wait_vm(0));
+
     // ---- epilogue
-    float l_tot[NB];
+    float l_tot[NB], m_out[NB];
 #pragma unroll
-    for (int rb = 0; rb < NB; ++rb) l_tot[rb] = sum_xor32(l_part[rb]);
+    for (int rb = 0; rb < NB; ++rb) {
+        l_tot[rb] = sum_xor32(l_part[rb]);
+        m_out[rb] = seen[rb] ? m_used[rb] : -INFINITY;
+    }
 
     if constexpr (KS > 1) {
         // key group 1 hands (O, m, l) to key group 0 through LDS; lane-major, conflict free
@@ -504,6 +604,7 @@ prefill_wide_kernel(PrefillArgs a)
                 const float c0 = mn == -INFINITY ? 0.f : fast_exp2(m0 - mn);
                 const float c1 = mn == -INFINITY ? 0.f : fast_exp2(m1 - mn);
                 l_tot[rb] = l_tot[rb] * c0 + l1 * c1;
+                m_out[rb] = mn;
 #pragma unroll
                 for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -513,6 +614,28 @@ prefill_wide_kernel(PrefillArgs a)
         }
     }
     if (kg != 0 || !wave_active) return;
+
+    if (a.n_splits > 1) {
+        // split-KV partial in the reference's format (qwen35_attn_part.comp:3): unnormalised
+        // O, then (m, l) with m in natural-log units; a row with no visible key in this split
+        // carries the reference's initial max and l = 0.  The combine kernel merges.
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb) {
+            const int qrow = w_first + 32 * rb + n;
+            if (qrow >= a.n_query) continue;
+            float* pr = a.part + (((size_t)qrow * a.n_q_heads + h) * a.n_splits + split) * (HD + 2);
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    const int dim = 32 * db + 8 * a4 + 4 * hh;
+                    *(f32x2*)(pr + dim) = f32x2{o[rb][db][4 * a4], o[rb][db][4 * a4 + 1]};
+                    *(f32x2*)(pr + dim + 2) = f32x2{o[rb][db][4 * a4 + 2], o[rb][db][4 * a4 + 3]};
+                }
+            if (hh == 0) *(f32x2*)(pr + HD) = f32x2{m_out[rb] > -INFINITY ? m_out[rb] * kLn2 : kNegBig, l_tot[rb]};
+        }
+        return;
+    }
 
     // lane (row n, hh) holds dims 32 db + 8 a4 + 4 hh + (0..3) of its row
 #pragma unroll
