@@ -291,8 +291,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": head["tflops"] / MFMA_F16_PEAK_TFLOPS,
                      "traffic": measured_traffic("cfg2"),
-                     "kernel": "nxa::prefill_kernel<128, f16 Q, f16 O> (one launch per call, timed with "
-                               "HIP events on its stream)",
+                     "kernel": "nxa::prefill_wide_kernel<128, KS=2, f16 Q, f16 O> (64-row blocks, key range "
+                               "over two waves; one launch per call, timed with HIP events on its stream)",
                      "algorithmic_gflop_per_call": head["gflop"]},
         "cpu_baseline": cpu,
         "extra": extra,
