@@ -117,9 +117,12 @@ long long decode_rows(const nexus_attn_desc* d)
 
 // 16-row tiles per workgroup: two when the rows need more than one tile, so a 32-row
 // verify batch (4 drafts x 8 heads) shares every K/V byte it reads.
+// Two 16-row tiles per workgroup up to head dim 128 (one K/V read feeds 32 rows); above that
+// one tile and more row groups, which keeps two waves per SIMD (the row groups of a split
+// read the same keys, through the XCD's L2 -- see default_decode_splits).
 int decode_row_tiles(const nexus_attn_desc* d)
 {
-    return decode_rows(d) > nxa::kDecodeRowTile ? nxa::kDecodeMaxRowTiles : 1;
+    return decode_rows(d) > nxa::kDecodeRowTile && d->head_dim <= 128 ? nxa::kDecodeMaxRowTiles : 1;
 }
 
 int decode_rowgroups(const nexus_attn_desc* d)
@@ -131,7 +134,7 @@ int decode_rowgroups(const nexus_attn_desc* d)
 // Workgroups resident at once per CU for the decode kernel (its register budget).
 int decode_wg_per_cu(const nexus_attn_desc* d)
 {
-    return d->head_dim * decode_row_tiles(d) <= 128 ? 2 : 1;     // decode_waves_per_simd
+    return d->head_dim * decode_row_tiles(d) <= 256 ? 2 : 1;     // decode_waves_per_simd
 }
 
 int default_decode_splits(const nexus_attn_desc* d)
@@ -147,6 +150,15 @@ int default_decode_splits(const nexus_attn_desc* d)
     if (s > by_len) s = by_len;
     if (s < 1) s = 1;
     if (s > kMaxSplits) s = kMaxSplits;
+    // Several row groups: workgroups are dealt to the 8 XCDs round-robin in grid order
+    // (split fastest, row group slowest), so the row groups of one (split, kv head) share an
+    // XCD -- and its L2 copy of their keys -- when splits x kv heads is a multiple of 8.
+    if (decode_rowgroups(d) > 1) {
+        long long m = 8;
+        for (long long h = d->n_kv_heads; h % 2 == 0 && m > 1; h /= 2) m /= 2;
+        s = (s + m - 1) / m * m;
+        if (s > kMaxSplits) s = kMaxSplits / m * m;
+    }
     return (int)s;
 }
 

@@ -30,7 +30,7 @@
 //    back as V^T A operands (16 bytes = 8 keys of one dim).
 //  * Software pipeline over register double buffers: K and V of step s + 2 are issued as
 //    soon as step s has consumed its K and V registers, so two steps (32 KB at hd 128) stay
-//    in flight per wave (one step for the largest tiles, hd x rows > 256).  The Q^T
+//    in flight per wave (one step from hd x rows > 128, with two waves per SIMD).  The Q^T
 //    operands (f16 high/low parts) sit in LDS, one copy per workgroup, which keeps the
 //    register budget at two waves per SIMD for hd 128.
 //  * The 4 waves merge their (m, l, O) through LDS before the partial is written.
@@ -39,10 +39,12 @@
 
 namespace nxa {
 
-// Register budget per (head_dim x row tiles): two waves per SIMD with K/V of two steps in
-// flight up to 128; one wave per SIMD with two steps up to 384; one step beyond that.
-constexpr int decode_waves_per_simd(int hd, int rt) { return hd * rt <= 128 ? 2 : 1; }
-constexpr int decode_depth(int hd, int rt) { return hd * rt <= 384 ? 2 : 1; }
+// Register budget per (head_dim x row tiles): two waves per SIMD up to 256 (two steps of K/V
+// in flight up to 128, one step above); one wave per SIMD beyond, which the host avoids for
+// head dims above 128 by using one row tile and more row groups (at one wave per SIMD the
+// compiler moves the accumulators through AGPRs on every step).
+constexpr int decode_waves_per_simd(int hd, int rt) { return hd * rt <= 256 ? 2 : 1; }
+constexpr int decode_depth(int hd, int rt) { return hd * rt <= 128 ? 2 : (hd * rt <= 256 ? 1 : (hd * rt <= 384 ? 2 : 1)); }
 
 template <int HD, int RT>
 struct DecodeLayout {
