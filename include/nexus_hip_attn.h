@@ -112,6 +112,23 @@ size_t nexus_hip_attn_decode_ws_bytes(const nexus_attn_desc* desc, int n_splits)
 /* The split count nexus_hip_attn_decode uses when called with n_splits <= 0. */
 int nexus_hip_attn_decode_default_splits(const nexus_attn_desc* desc);
 
+/* The two calls above with the output gate of the gated attention layers fused into the
+ * epilogue: out = attention * sigmoid(gate), with sigmoid clamped to 1 above 80 and to 0
+ * below -80.  Replaces the gate of qwen35_attn_comb.comp:34-38 (decode, inside the
+ * combine) and the post-gate of the batched prefill (src/model/transformer.h:8502-8515).
+ * gate: f32 [n_query][n_q_heads][head_dim] on the device, 16-byte aligned; NULL = no gate
+ * (the plain entries above). */
+int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc,
+                                 const void* q, const uint16_t* k, const uint16_t* v,
+                                 const float* gate, void* out,
+                                 void* workspace, size_t workspace_bytes,
+                                 nexus_stream_t stream);
+int nexus_hip_attn_decode_gated(const nexus_attn_desc* desc,
+                                const void* q, const uint16_t* k, const uint16_t* v,
+                                const float* gate, void* out,
+                                float* partial_ws, int n_splits,
+                                nexus_stream_t stream);
+
 /* Message for the last non-zero status on the calling thread ("" if none). */
 const char* nexus_hip_attn_last_error(void);
 /* Library version, e.g. "nexus_hip_attn 0.1.0 gfx950". */

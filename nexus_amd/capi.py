@@ -30,6 +30,8 @@ EXPORTED_SYMBOLS = (
     "nexus_hip_attn_decode",
     "nexus_hip_attn_decode_ws_bytes",
     "nexus_hip_attn_decode_default_splits",
+    "nexus_hip_attn_prefill_gated",
+    "nexus_hip_attn_decode_gated",
     "nexus_hip_attn_last_error",
     "nexus_hip_attn_version",
 )
@@ -94,6 +96,10 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.nexus_hip_attn_decode_ws_bytes.restype = sz
     lib.nexus_hip_attn_decode_default_splits.argtypes = [dp]
     lib.nexus_hip_attn_decode_default_splits.restype = ctypes.c_int
+    lib.nexus_hip_attn_prefill_gated.argtypes = [dp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.nexus_hip_attn_prefill_gated.restype = ctypes.c_int
+    lib.nexus_hip_attn_decode_gated.argtypes = [dp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
+    lib.nexus_hip_attn_decode_gated.restype = ctypes.c_int
     lib.nexus_hip_attn_last_error.argtypes = []
     lib.nexus_hip_attn_last_error.restype = ctypes.c_char_p
     lib.nexus_hip_attn_version.argtypes = []
@@ -130,14 +136,22 @@ def decode_default_splits(desc: AttnDesc) -> int:
 
 
 def prefill_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, ws: int, ws_bytes: int,
-                stream: int, check: bool = True) -> int:
-    rc = load().nexus_hip_attn_prefill(ctypes.byref(desc), q, k, v, out, ws, ws_bytes, stream)
+                stream: int, check: bool = True, gate: int = 0) -> int:
+    lib = load()
+    if gate:
+        rc = lib.nexus_hip_attn_prefill_gated(ctypes.byref(desc), q, k, v, gate, out, ws, ws_bytes, stream)
+    else:
+        rc = lib.nexus_hip_attn_prefill(ctypes.byref(desc), q, k, v, out, ws, ws_bytes, stream)
     return _check(rc) if check else rc
 
 
 def decode_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, ws: int, n_splits: int,
-               stream: int, check: bool = True) -> int:
-    rc = load().nexus_hip_attn_decode(ctypes.byref(desc), q, k, v, out, ws, int(n_splits), stream)
+               stream: int, check: bool = True, gate: int = 0) -> int:
+    lib = load()
+    if gate:
+        rc = lib.nexus_hip_attn_decode_gated(ctypes.byref(desc), q, k, v, gate, out, ws, int(n_splits), stream)
+    else:
+        rc = lib.nexus_hip_attn_decode(ctypes.byref(desc), q, k, v, out, ws, int(n_splits), stream)
     return _check(rc) if check else rc
 
 

@@ -221,11 +221,13 @@ bool small_query_path(const nexus_attn_desc* d)
     return decode_rows(d) <= (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
 }
 
-int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, int n_splits, hipStream_t stream)
+int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, const float* gate, int n_splits,
+                       hipStream_t stream)
 {
     nxa::CombineArgs c{};
     c.part = ws;
     c.out = out;
+    c.gate = gate;
     c.n_rows = d->n_query * d->n_q_heads;
     c.n_splits = n_splits;
     const hipError_t e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
@@ -234,7 +236,7 @@ int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, int n_spl
 }
 
 int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const uint16_t* v, void* out,
-               float* ws, int n_splits, hipStream_t stream)
+               const float* gate, float* ws, int n_splits, hipStream_t stream)
 {
     int kb, ke;
     key_range(d, &kb, &ke);
@@ -248,6 +250,7 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.k = k;
     a.v = v;
     a.out = out;
+    a.gate = gate;
     a.part = ws;
     a.kv_stride = d->kv_row_stride;
     a.n_q_heads = d->n_q_heads;
@@ -270,7 +273,7 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
                                       is_ext(d), decode_rowgroups(d), stream);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
     if (n_splits > 1) {
-        const int rc = launch_combine_for(d, ws, out, n_splits, stream);
+        const int rc = launch_combine_for(d, ws, out, gate, n_splits, stream);
         if (rc != NEXUS_OK) return rc;
     }
     return ok();
@@ -294,17 +297,25 @@ int nexus_hip_attn_decode_default_splits(const nexus_attn_desc* desc)
     return default_decode_splits(desc);
 }
 
-int nexus_hip_attn_decode(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
-                          const uint16_t* v, void* out, float* partial_ws, int n_splits,
-                          nexus_stream_t stream)
+int nexus_hip_attn_decode_gated(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
+                                const uint16_t* v, const float* gate, void* out, float* partial_ws,
+                                int n_splits, nexus_stream_t stream)
 {
     const int rc = check_desc(desc);
     if (rc != NEXUS_OK) return rc;
     if (!q || !k || !v || !out) return fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
     if (!partial_ws) return fail(NEXUS_E_WORKSPACE, "partial_ws is NULL");
+    if (gate && ((uintptr_t)gate & 15u)) return fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
     if (n_splits <= 0) n_splits = default_decode_splits(desc);
     if (n_splits > kMaxSplits) return fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
-    return run_decode(desc, q, k, v, out, partial_ws, n_splits, (hipStream_t)stream);
+    return run_decode(desc, q, k, v, out, gate, partial_ws, n_splits, (hipStream_t)stream);
+}
+
+int nexus_hip_attn_decode(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
+                          const uint16_t* v, void* out, float* partial_ws, int n_splits,
+                          nexus_stream_t stream)
+{
+    return nexus_hip_attn_decode_gated(desc, q, k, v, nullptr, out, partial_ws, n_splits, stream);
 }
 
 size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
@@ -316,13 +327,14 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
     return prefill_split_ws_bytes(desc, s);
 }
 
-int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
-                           const uint16_t* v, void* out, void* workspace, size_t workspace_bytes,
-                           nexus_stream_t stream)
+int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
+                                 const uint16_t* v, const float* gate, void* out, void* workspace,
+                                 size_t workspace_bytes, nexus_stream_t stream)
 {
     const int rc = check_desc(desc);
     if (rc != NEXUS_OK) return rc;
     if (!q || !k || !v || !out) return fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
+    if (gate && ((uintptr_t)gate & 15u)) return fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
 
     // A handful of queries (speculative verify, tiny prompts): the split-KV kernel fills
@@ -330,7 +342,7 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     if (small_query_path(desc) && workspace) {
         const int splits = default_decode_splits(desc);
         if (workspace_bytes >= decode_ws_bytes(desc, splits))
-            return run_decode(desc, q, k, v, out, (float*)workspace, splits, s);
+            return run_decode(desc, q, k, v, out, gate, (float*)workspace, splits, s);
     }
 
     const PrefillPlan plan = prefill_plan(desc);
@@ -342,6 +354,7 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
     a.k = k;
     a.v = v;
     a.out = out;
+    a.gate = gate;
     a.part = (float*)workspace;
     a.kv_stride = desc->kv_row_stride;
     a.n_q_heads = desc->n_q_heads;
@@ -365,10 +378,17 @@ int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uin
                              : nxa::launch_prefill(a, desc->head_dim, q32, o32, is_ext(desc), s);
     if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
     if (splits > 1) {
-        const int rc2 = launch_combine_for(desc, (float*)workspace, out, splits, s);
+        const int rc2 = launch_combine_for(desc, (float*)workspace, out, gate, splits, s);
         if (rc2 != NEXUS_OK) return rc2;
     }
     return ok();
+}
+
+int nexus_hip_attn_prefill(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
+                           const uint16_t* v, void* out, void* workspace, size_t workspace_bytes,
+                           nexus_stream_t stream)
+{
+    return nexus_hip_attn_prefill_gated(desc, q, k, v, nullptr, out, workspace, workspace_bytes, stream);
 }
 
 const char* nexus_hip_attn_last_error(void) { return g_last_error; }

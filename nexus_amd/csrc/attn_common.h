@@ -114,6 +114,27 @@ constexpr uint32_t kSelHi = 0x07060302u;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Output gate of the gated attention layers: sigmoid(z), clamped to 1 above z = 80 and to 0
+// below -80 (qwen35_attn_comb.comp:34-38; the CPU path, transformer.h:8508-8511).
+__device__ __forceinline__ float gate_sigmoid(float z)
+{
+    return z > 80.f ? 1.f : (z < -80.f ? 0.f : 1.f / (1.f + fast_exp2(-z * kLog2e)));
+}
+// Gate factors of 4 (or 2) consecutive output elements starting at `off` (16- or 8-byte
+// aligned); all 1 when the call has no gate.
+__device__ __forceinline__ f32x4 gate4(const float* gate, size_t off)
+{
+    if (!gate) return f32x4{1.f, 1.f, 1.f, 1.f};
+    const f32x4 z = *(const f32x4*)(gate + off);
+    return f32x4{gate_sigmoid(z[0]), gate_sigmoid(z[1]), gate_sigmoid(z[2]), gate_sigmoid(z[3])};
+}
+__device__ __forceinline__ f32x2 gate2(const float* gate, size_t off)
+{
+    if (!gate) return f32x2{1.f, 1.f};
+    const f32x2 z = *(const f32x2*)(gate + off);
+    return f32x2{gate_sigmoid(z[0]), gate_sigmoid(z[1])};
+}
+
 // Order this wave's LDS writes before its later LDS reads (wave-private LDS regions).
 __device__ __forceinline__ void wave_lds_sync()
 {

@@ -373,7 +373,7 @@ decode_part_kernel(DecodeArgs a)
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const int dim = 16 * dt + 4 * g;
-                const f32x4 y = o[rt][dt] * inv;
+                const f32x4 y = o[rt][dt] * inv * gate4(a.gate, prow * HD + dim);
                 if constexpr (O_F32) {
                     *(f32x4*)((float*)a.out + prow * HD + dim) = y;
                 } else {
@@ -473,7 +473,7 @@ combine_kernel(CombineArgs a)
         }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    const f32x2 y = acc * inv;
+    const f32x2 y = acc * inv * gate2(a.gate, (size_t)row * HD + 2 * dp);
     if constexpr (O_F32) {
         *(f32x2*)((float*)a.out + (size_t)row * HD + 2 * dp) = y;
     } else {

@@ -27,6 +27,7 @@ struct PrefillArgs {
     const uint16_t* k;
     const uint16_t* v;
     void* out;
+    const float* gate;              // [n_query][Hq][hd] f32 or null: out *= sigmoid(gate)
     float* part;                    // [n_query*Hq][n_splits][hd+2] partials (n_splits > 1)
     long long kv_stride;            // tokens between kv heads
     int n_q_heads, n_kv_heads, group;
@@ -43,6 +44,7 @@ struct DecodeArgs {
     const uint16_t* k;
     const uint16_t* v;
     void* out;                      // [n_query][Hq][hd]
+    const float* gate;              // [n_query][Hq][hd] f32 or null (applied with one split)
     float* part;                    // [n_query*Hq][n_splits][hd+2] (n_splits > 1)
     long long kv_stride;
     int n_q_heads, n_kv_heads, group;
@@ -60,6 +62,7 @@ struct DecodeArgs {
 struct CombineArgs {
     const float* part;              // [n_rows][n_splits][hd+2]
     void* out;                      // [n_rows][hd], row = qi*Hq + h
+    const float* gate;              // [n_rows][hd] f32 or null: out *= sigmoid(gate)
     int n_rows, n_splits;
 };
 

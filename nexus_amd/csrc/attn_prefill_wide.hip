@@ -649,8 +649,9 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
             for (int a4 = 0; a4 < 4; ++a4) {
                 const int dim = 32 * db + 8 * a4 + 4 * hh;
-                const float v0 = o[rb][db][4 * a4] * inv, v1 = o[rb][db][4 * a4 + 1] * inv;
-                const float v2 = o[rb][db][4 * a4 + 2] * inv, v3 = o[rb][db][4 * a4 + 3] * inv;
+                const f32x4 gt = gate4(a.gate, obase + dim);
+                const float v0 = o[rb][db][4 * a4] * inv * gt[0], v1 = o[rb][db][4 * a4 + 1] * inv * gt[1];
+                const float v2 = o[rb][db][4 * a4 + 2] * inv * gt[2], v3 = o[rb][db][4 * a4 + 3] * inv * gt[3];
                 if constexpr (O_F32) {
                     *(f32x4*)((float*)a.out + obase + dim) = f32x4{v0, v1, v2, v3};
                 } else {

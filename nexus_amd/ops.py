@@ -49,12 +49,24 @@ def make_desc_for(q: torch.Tensor, k: torch.Tensor, *, n_kv_heads: int, q_base_p
                           softcap=softcap, q_dtype=_DT[q.dtype], o_dtype=_DT[od])
 
 
+def _gate_ptr(gate: torch.Tensor | None, q: torch.Tensor) -> int:
+    if gate is None:
+        return 0
+    if gate.dtype != torch.float32 or gate.shape != q.shape or not gate.is_contiguous() or gate.device != q.device:
+        raise ValueError("gate must be a contiguous float32 tensor shaped like q on q's device")
+    return gate.data_ptr()
+
+
 def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads: int,
                  q_base_pos: int, n_ctx: int, sliding_window: int = 0, scale: float = 0.0,
                  softcap: float = 0.0, out: torch.Tensor | None = None,
                  out_dtype: torch.dtype | None = None,
-                 workspace: torch.Tensor | None = None, split: bool = True) -> torch.Tensor:
+                 workspace: torch.Tensor | None = None, split: bool = True,
+                 gate: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal GQA prefill (nexus_hip_attn_prefill); `gate` (f32, q's shape) multiplies the
+    output by sigmoid(gate) clamped at +-80 (nexus_hip_attn_prefill_gated)."""
     _check_tensors(q, k, v, n_kv_heads)
+    gate_ptr = _gate_ptr(gate, q)
     desc = make_desc_for(q, k, n_kv_heads=n_kv_heads, q_base_pos=q_base_pos, n_ctx=n_ctx,
                          sliding_window=sliding_window, scale=scale, softcap=softcap,
                          out_dtype=out_dtype if out is None else out.dtype)
@@ -69,7 +81,7 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_head
             ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(q.device).cuda_stream
     capi.prefill_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws_ptr,
-                     ws_bytes, stream)
+                     ws_bytes, stream, gate=gate_ptr)
     return out
 
 
@@ -77,8 +89,11 @@ def attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads
                 q_base_pos: int, n_ctx: int, n_splits: int = 0, sliding_window: int = 0,
                 scale: float = 0.0, softcap: float = 0.0, out: torch.Tensor | None = None,
                 out_dtype: torch.dtype | None = None,
-                partial_ws: torch.Tensor | None = None) -> torch.Tensor:
+                partial_ws: torch.Tensor | None = None,
+                gate: torch.Tensor | None = None) -> torch.Tensor:
+    """Split-KV decode / verify (nexus_hip_attn_decode); `gate` as in attn_prefill."""
     _check_tensors(q, k, v, n_kv_heads)
+    gate_ptr = _gate_ptr(gate, q)
     desc = make_desc_for(q, k, n_kv_heads=n_kv_heads, q_base_pos=q_base_pos, n_ctx=n_ctx,
                          sliding_window=sliding_window, scale=scale, softcap=softcap,
                          out_dtype=out_dtype or (out.dtype if out is not None else torch.float32))
@@ -91,5 +106,5 @@ def attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads
         partial_ws = torch.empty(need // 4, dtype=torch.float32, device=q.device)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     capi.decode_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                    partial_ws.data_ptr(), n_splits, stream)
+                    partial_ws.data_ptr(), n_splits, stream, gate=gate_ptr)
     return out

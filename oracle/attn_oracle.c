@@ -14,6 +14,14 @@
  *                         softcap via fast_tanh/attn_softcap attention.h:232-245
  *   oracle_split_partials gpu/shaders/qwen35_attn_part.comp:1-108 (partial (acc, m, l))
  *   oracle_split_combine  gpu/shaders/qwen35_attn_comb.comp:1-41 (LSE merge, no gate)
+ *   oracle_gate_mul       model/transformer.h:8505-8512 (post-gate of the batched prefill;
+ *                         the same clamped sigmoid as qwen35_attn_comb.comp:34-38)
+ *   oracle_decode_prep    gpu/shaders/qwen35_attn_prep.comp:1-101 for one token: per-head
+ *                         RMSNorm as cpu::rms_norm (cpu/matmul.h:1860-1880) or
+ *                         nx_rms_norm_add_one (model/transformer.h:504-520), selected as
+ *                         nx_apply_projection_norm_inplace does (transformer.h:580-618);
+ *                         RoPE as rope_apply (model/attention.h:491-608) with the angle table
+ *                         supplied; K/V store with kvcache.h:903-911 or :256-274 conversion
  *   oracle_naive_f64      independent float64 brute force (checker only)
  *
  * How each function is pinned (tests/test_oracle.py):
@@ -26,7 +34,12 @@
  *   attn_batch     every row against the reference's forward_cached_scores at that
  *                  query's position, against float64 brute force, and against closed
  *                  forms (one key, zero query, one-hot key, window of one);
- *   split/combine  split-vs-unsplit identity (LSE associativity) for many chunkings.
+ *   split/combine  split-vs-unsplit identity (LSE associativity) for many chunkings;
+ *   gate_mul       against scipy's expit inside (-80, 80) and the clamp values outside;
+ *   decode_prep    norm against the reference's own cpu::rms_norm (oracle/_ref), the (1+w)
+ *                  form against it with 1+w weights; RoPE against the reference's own
+ *                  rope_apply with the same angles, identity/composition/norm-preserving
+ *                  invariants and the neox<->interleaved permutation; stores as above.
  */
 #include "attn_oracle.h"
 
@@ -302,6 +315,87 @@ void oracle_split_combine(const float* part, float* out, int n_rows, int head_di
             out[(size_t)r * head_dim + d] = L > 0.f ? a / L : 0.f;
         }
     }
+}
+
+/* -------------------------------------------------------------------- output gate */
+
+/* out[i] *= sigmoid(gate[i]) with the clamp of model/transformer.h:8508-8510. */
+void oracle_gate_mul(float* out, const float* gate, size_t n)
+{
+    for (size_t i = 0; i < n; ++i) {
+        const float z = gate[i];
+        const float s = (z > 80.0f) ? 1.0f : (z < -80.0f) ? 0.0f : 1.0f / (1.0f + expf(-z));
+        out[i] *= s;
+    }
+}
+
+/* ------------------------------------------------------------------- decode prep */
+
+/* RMSNorm of one head row in place.  zc = 0: (x * w) * inv as cpu::rms_norm
+ * (cpu/matmul.h:1876-1880); zc = 1: x * inv * (1 + w) as nx_rms_norm_add_one
+ * (model/transformer.h:511-520).  inv = 1 / sqrtf(sum x^2 / n + eps). */
+static void head_rms_norm(float* x, const float* w, int n, float eps, int zc)
+{
+    float ss = 0.0f;
+    for (int i = 0; i < n; ++i) ss += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = 0; i < n; ++i) x[i] = zc ? x[i] * inv * (1.0f + w[i]) : (x[i] * w[i]) * inv;
+}
+
+/* RoPE of the first `rot` dims of one head row in place, angles from tab (cos at tab[i],
+ * sin at tab[rot/2 + i]); interleaved pairs (2i, 2i+1) or rotate_half pairs (i, i + rot/2),
+ * the two layouts of rope_apply (model/attention.h:593-608). */
+static void head_rope(float* x, int rot, const float* tab, int interleaved)
+{
+    const int half = rot / 2;
+    for (int i = 0; i < half; ++i) {
+        const float c = tab[i], s = tab[half + i];
+        if (interleaved) {
+            const float x0 = x[2 * i], x1 = x[2 * i + 1];
+            x[2 * i] = x0 * c - x1 * s;
+            x[2 * i + 1] = x0 * s + x1 * c;
+        } else {
+            const float x0 = x[i], x1 = x[i + half];
+            x[i] = x0 * c - x1 * s;
+            x[i + half] = x1 * c + x0 * s;
+        }
+    }
+}
+
+/* One token of qwen35_attn_prep.comp.  qg: per head [q(hd) | gate(hd)] (flags & 4: plain q
+ * [n_heads][hd]); kraw/vraw [n_kv][hd]; qnw/knw [hd] (unused when the norm is off);
+ * tab [rot].  Writes q_out [n_heads][hd], gate_out [n_heads][hd] (gated layers), the f16
+ * bits of K and V into kc/vc [n_kv][cap][hd] at row `pos`, and kv_out [2][n_kv][hd] (f32
+ * K then V as stored).  flags: 1 q norm (1+w), 2 k norm (1+w), 4 no gate, 8 no q norm,
+ * 16 no k norm, 32 interleaved RoPE.  rne = 0: truncating store (kvcache.h:903-911). */
+void oracle_decode_prep(int n_heads, int n_kv, int hd, int rot, int flags, float eps, int pos, long cap,
+                        const float* qg, const float* kraw, const float* vraw,
+                        const float* qnw, const float* knw, const float* tab,
+                        float* q_out, float* gate_out, uint16_t* kc, uint16_t* vc, float* kv_out, int rne)
+{
+    const int gated = (flags & 4) == 0, inter = (flags & 32) != 0;
+    float* row = (float*)malloc((size_t)hd * sizeof(float));
+    for (int h = 0; h < n_heads; ++h) {
+        const float* src = gated ? qg + (size_t)h * 2 * hd : qg + (size_t)h * hd;
+        memcpy(row, src, (size_t)hd * sizeof(float));
+        if (gated) memcpy(gate_out + (size_t)h * hd, src + hd, (size_t)hd * sizeof(float));
+        if (!(flags & 8)) head_rms_norm(row, qnw, hd, eps, flags & 1);
+        head_rope(row, rot, tab, inter);
+        memcpy(q_out + (size_t)h * hd, row, (size_t)hd * sizeof(float));
+    }
+    for (int which = 0; which < 2; ++which) {
+        for (int h = 0; h < n_kv; ++h) {
+            memcpy(row, (which ? vraw : kraw) + (size_t)h * hd, (size_t)hd * sizeof(float));
+            if (which == 0) {
+                if (!(flags & 16)) head_rms_norm(row, knw, hd, eps, flags & 2);
+                head_rope(row, rot, tab, inter);
+            }
+            uint16_t* dst = (which ? vc : kc) + ((size_t)h * cap + pos) * hd;
+            for (int d = 0; d < hd; ++d) dst[d] = rne ? nx_f32_to_f16_rne(row[d]) : nx_f32_to_f16_trunc(row[d]);
+            memcpy(kv_out + ((size_t)which * n_kv + h) * hd, row, (size_t)hd * sizeof(float));
+        }
+    }
+    free(row);
 }
 
 /* ------------------------------------------------------------ float64 brute force */

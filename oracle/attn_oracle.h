@@ -70,6 +70,13 @@ void oracle_split_partials(const float* Q, const uint16_t* K, const uint16_t* V,
 /* qwen35_attn_comb.comp:1-41 without the gate: out = sum_c acc_c e^{m_c-M} / sum_c l_c e^{m_c-M}. */
 void oracle_split_combine(const float* part, float* out, int n_rows, int head_dim, int n_chunks);
 
+void oracle_gate_mul(float* out, const float* gate, size_t n);
+
+void oracle_decode_prep(int n_heads, int n_kv, int hd, int rot, int flags, float eps, int pos, long cap,
+                        const float* qg, const float* kraw, const float* vraw,
+                        const float* qnw, const float* knw, const float* tab,
+                        float* q_out, float* gate_out, uint16_t* kc, uint16_t* vc, float* kv_out, int rne);
+
 /* Independent checker: float64 naive softmax attention with the same mask rules. */
 void oracle_naive_f64(const float* Q, const uint16_t* K, const uint16_t* V, double* Out,
                       int n_q_heads, int n_kv_heads, int head_dim,

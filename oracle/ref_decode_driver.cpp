@@ -8,6 +8,8 @@
 //                                                          model/kvcache.h:69-78,148-178,214-241,655-672
 //   nexus::model::KVCache::f32_to_f16_rne                  model/kvcache.h:256-274
 //   nexus::quant::f16_to_f32                               gguf/quant.h:128-161
+//   nexus::cpu::rms_norm                                   cpu/matmul.h:1860-1880
+//   nexus::model::rope_apply                               model/attention.h:491-608
 // Transformer::attn_batch_cpu (model/transformer.h:8653-8685) is NOT built: its header
 // pulls in the Vulkan backend and the prebuilt SPIR-V blob headers, so it is restated
 // in attn_oracle.c and pinned against forward_cached_scores row by row instead.
@@ -77,5 +79,19 @@ long ref_kv_capacity_after(int n_tok, int head_dim)
 uint16_t ref_f32_to_f16_rne(float f) { return KVCache::f32_to_f16_rne(f); }
 
 float ref_f16_to_f32(uint16_t h) { return nexus::quant::f16_to_f32(h); }
+
+void ref_rms_norm(const float* x, const float* w, float* y, long n, float eps)
+{
+    nexus::cpu::rms_norm(x, w, y, (size_t)n, eps);
+}
+
+// Standard RoPE (type 0) of one head in place; layout 0 = interleaved, 1 = rotate_half.
+void ref_rope_apply(float* x, int pos, int head_dim, float freq_base, int layout)
+{
+    nexus::model::RoPEConfig cfg;
+    cfg.freq_base = freq_base;
+    cfg.layout = layout;
+    nexus::model::rope_apply(x, pos, head_dim, cfg);
+}
 
 }  // extern "C"

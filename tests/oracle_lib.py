@@ -46,6 +46,9 @@ def oracle() -> ctypes.CDLL:
         lib.oracle_split_partials.argtypes = [_f32p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _l, _i, _i, _f, _i, _i]
         lib.oracle_split_combine.argtypes = [_f32p, _f32p, _i, _i, _i]
         lib.oracle_naive_f64.argtypes = [_f32p, _u16p, _u16p, _f64p, _i, _i, _i, _i, _l, _i, _i, _i, _d, _d]
+        lib.oracle_gate_mul.argtypes = [_f32p, _f32p, ctypes.c_size_t]
+        lib.oracle_decode_prep.argtypes = [_i, _i, _i, _i, _i, _f, _i, _l, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           _f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _i]
         _oracle = lib
     return _oracle
 
@@ -70,6 +73,8 @@ def ref() -> ctypes.CDLL:
         lib.ref_f32_to_f16_rne.restype = ctypes.c_uint16
         lib.ref_f16_to_f32.argtypes = [ctypes.c_uint16]
         lib.ref_f16_to_f32.restype = _f
+        lib.ref_rms_norm.argtypes = [_f32p, _f32p, _f32p, _l, _f]
+        lib.ref_rope_apply.argtypes = [_f32p, _i, _i, _f, _i]
         _ref = lib
     return _ref
 
@@ -137,6 +142,51 @@ def split_combine(part):
     out = np.zeros((rows, hd2 - 2), np.float32)
     oracle().oracle_split_combine(part, out, rows, hd2 - 2, n_chunks)
     return out
+
+
+def gate_mul(out, gate):
+    """out * sigmoid(gate) with the reference's clamp (oracle_gate_mul)."""
+    out = _c(out, np.float32).copy()
+    gate = _c(gate, np.float32)
+    assert out.shape == gate.shape
+    oracle().oracle_gate_mul(out.reshape(-1), gate.reshape(-1), out.size)
+    return out
+
+
+# decode-prep flags (qwen35_attn_prep.comp:7-8)
+PREP_Q_ZC, PREP_K_ZC, PREP_NO_GATE, PREP_NO_QNORM, PREP_NO_KNORM, PREP_INTERLEAVED = 1, 2, 4, 8, 16, 32
+
+
+def decode_prep(qg, kraw, vraw, qnw, knw, tab, *, n_heads, n_kv, hd, rot, flags, eps, pos, cap,
+                kc=None, vc=None, rne=False):
+    """One token of the decode prep (oracle_decode_prep).  Returns (q_out, gate_out, kc, vc,
+    kv_out); kc/vc are [n_kv][cap][hd] f16 bit arrays (updated copies when given)."""
+    qg, kraw, vraw = _c(qg, np.float32).reshape(-1), _c(kraw, np.float32).reshape(-1), _c(vraw, np.float32).reshape(-1)
+    qnw = _c(qnw if qnw is not None else np.zeros(hd), np.float32)
+    knw = _c(knw if knw is not None else np.zeros(hd), np.float32)
+    tab = _c(tab, np.float32)
+    q_out = np.zeros(n_heads * hd, np.float32)
+    gate_out = np.zeros(n_heads * hd, np.float32)
+    kc = np.zeros(n_kv * cap * hd, np.uint16) if kc is None else _c(kc, np.uint16).reshape(-1).copy()
+    vc = np.zeros(n_kv * cap * hd, np.uint16) if vc is None else _c(vc, np.uint16).reshape(-1).copy()
+    kv_out = np.zeros(2 * n_kv * hd, np.float32)
+    oracle().oracle_decode_prep(n_heads, n_kv, hd, rot, flags, eps, pos, cap, qg, kraw, vraw, qnw, knw, tab,
+                                q_out, gate_out, kc, vc, kv_out, 1 if rne else 0)
+    return (q_out.reshape(n_heads, hd), gate_out.reshape(n_heads, hd), kc.reshape(n_kv, cap, hd),
+            vc.reshape(n_kv, cap, hd), kv_out.reshape(2, n_kv, hd))
+
+
+def ref_rms_norm(x, w, eps):
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    y = np.zeros_like(x)
+    ref().ref_rms_norm(x, w, y, x.size, eps)
+    return y
+
+
+def ref_rope(x, pos, head_dim, base, layout):
+    x = _c(x, np.float32).copy()
+    ref().ref_rope_apply(x, pos, head_dim, base, layout)
+    return x
 
 
 def naive_f64(q, k, v, *, n_kv_heads, n_ctx, q_base_pos, sliding_window=0, scale=0.0, softcap=0.0):

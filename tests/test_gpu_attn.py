@@ -30,22 +30,34 @@ def assert_close(got, ref, what=""):
     assert ma < MAX_ABS and rl < REL_L2, f"{what}: max_abs={ma:.3e} rel_l2={rl:.3e}"
 
 
-def run_prefill(q, k, v, *, hkv, n_ctx, q_base, q_f16=False, o_f16=False, sw=0, cap=0.0, split=True):
+def run_prefill(q, k, v, *, hkv, n_ctx, q_base, q_f16=False, o_f16=False, sw=0, cap=0.0, split=True, gate=None):
     qt = dev(q)
     if q_f16:
         qt = qt.half()
     out = ops.attn_prefill(qt, dev(k), dev(v), n_kv_heads=hkv, q_base_pos=q_base, n_ctx=n_ctx,
                            sliding_window=sw, softcap=cap, out_dtype=torch.float16 if o_f16 else torch.float32,
-                           split=split)
+                           split=split, gate=None if gate is None else dev(gate))
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
 
-def run_decode(q, k, v, *, hkv, n_ctx, q_base, n_splits=0, sw=0, cap=0.0, ws=None):
+def run_decode(q, k, v, *, hkv, n_ctx, q_base, n_splits=0, sw=0, cap=0.0, ws=None, gate=None, o_f16=False):
     out = ops.attn_decode(dev(q), dev(k), dev(v), n_kv_heads=hkv, q_base_pos=q_base, n_ctx=n_ctx,
-                          n_splits=n_splits, sliding_window=sw, softcap=cap, partial_ws=ws)
+                          n_splits=n_splits, sliding_window=sw, softcap=cap, partial_ws=ws,
+                          gate=None if gate is None else dev(gate),
+                          out_dtype=torch.float16 if o_f16 else torch.float32)
     torch.cuda.synchronize()
-    return out.cpu().numpy()
+    return out.float().cpu().numpy()
+
+
+def make_gate(shape, seed):
+    """Gate logits over the sigmoid's whole range plus entries beyond the +-80 clamps."""
+    rng = np.random.default_rng(seed)
+    z = (rng.standard_normal(shape) * 4).astype(np.float32)
+    flat = z.reshape(-1)
+    idx = rng.choice(flat.size, size=max(1, flat.size // 50), replace=False)
+    flat[idx] = rng.choice(np.array([-1e4, -81.0, 81.0, 1e4], np.float32), size=idx.size)
+    return z
 
 
 # ------------------------------------------------------------------------ prefill
@@ -115,6 +127,30 @@ def test_prefill_chunked_equals_cold_rows(hip):
     cold = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=0, q_f16=True, split=False)
     chunk = run_prefill(q[base:], k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, split=False)
     assert O.max_abs(chunk, cold[base:]) < 1e-3
+
+
+GATED_PREFILL_CASES = [
+    # (Hq, Hkv, hd, n_query, q_base, q_f16, o_f16, sw, cap, split) -- one per epilogue
+    (64, 8, 128, 520, 37, False, False, 0, 0.0, True),     # pipelined kernel, 128-row blocks, f32 out
+    (8, 2, 128, 80, 0, True, True, 0, 0.0, True),          # pipelined kernel, 64-row blocks (key-group merge)
+    (16, 2, 256, 96, 40, True, True, 0, 0.0, True),        # general kernel, hd 256
+    (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # general kernel, softcap
+    (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # general kernel's key split + combine
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,qf16,of16,sw,cap,split", GATED_PREFILL_CASES)
+def test_prefill_gated(hip, hq, hkv, hd, nq, base, qf16, of16, sw, cap, split):
+    """out * sigmoid(gate) fused into every prefill epilogue (qwen35_attn_comb.comp:34-38)."""
+    n_ctx = base + nq
+    print(f"[case] prefill gated hq={hq} hkv={hkv} hd={hd} nq={nq} base={base} cap={cap}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=nq + 7, q_f16=qf16)
+    gate = make_gate(q.shape, nq)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, q_f16=qf16, o_f16=of16, sw=sw, cap=cap,
+                      split=split, gate=gate)
+    ref = O.gate_mul(O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, sliding_window=sw,
+                                  softcap=cap, n_threads=8), gate)
+    assert_close(got, ref, f"prefill gated {hq}/{hkv} hd{hd} nq{nq}@{base}")
 
 
 # ------------------------------------------------------------------------ decode
@@ -274,3 +310,28 @@ def test_verify_full_cfg5(hip):
     got = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base)      # routed to split-KV
     ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base, n_threads=8)
     assert_close(got, ref, "cfg5 full")
+
+
+GATED_DECODE_CASES = [
+    # (Hq, Hkv, hd, n_query, q_base, n_ctx, n_splits, o_f16)
+    (40, 8, 128, 1, 3000, 3001, 1, False),      # one split: the kernel writes the output itself
+    (40, 8, 128, 1, 3000, 3001, 64, True),      # split-KV: the combine applies the gate, f16 out
+    (16, 2, 256, 4, 2000, 2004, 0, False),      # MTP verify layout
+    (64, 1, 128, 1, 500, 501, 0, False),        # two row groups
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,n_ctx,splits,of16", GATED_DECODE_CASES)
+def test_decode_gated(hip, hq, hkv, hd, nq, base, n_ctx, splits, of16):
+    """Gated decode (transformer.h:8502-8515): the split combine or the single-split epilogue
+    multiplies by sigmoid(gate)."""
+    print(f"[case] decode gated hq={hq} hkv={hkv} hd={hd} nq={nq} ctx={n_ctx} splits={splits}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=n_ctx + 1)
+    gate = make_gate(q.shape, n_ctx)
+    got = run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits, gate=gate, o_f16=of16)
+    ref = O.gate_mul(O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8), gate)
+    assert_close(got, ref, f"decode gated {hq}/{hkv} hd{hd} nq{nq} splits{splits}")
+    plain = run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits, o_f16=of16)
+    sat = np.abs(gate) > 80
+    np.testing.assert_array_equal(got[sat & (gate > 0)], plain[sat & (gate > 0)])
+    assert not np.any(got[sat & (gate < 0)])

@@ -306,3 +306,122 @@ def test_split_partials_causal_drafts():
     y = O.split_combine(part).reshape(nq, hq, hd)
     r = O.naive_f64(q, k, v, n_kv_heads=hkv, n_ctx=base + nq, q_base_pos=base)
     assert O.max_abs(y, r) < 1e-5
+
+
+# ------------------------------------------------------------------ output gate, decode prep
+
+def test_gate_mul_sigmoid_and_clamps():
+    """oracle_gate_mul == out * expit(gate) inside (-80, 80); exactly out / 0 beyond."""
+    from scipy.special import expit
+    rng = np.random.default_rng(11)
+    z = rng.uniform(-79.9, 79.9, 4096).astype(np.float32)
+    out = rng.standard_normal(4096).astype(np.float32)
+    got = O.gate_mul(out, z)
+    np.testing.assert_allclose(got, out * expit(z.astype(np.float64)), rtol=2e-6, atol=1e-30)
+    z2 = np.array([80.5, 1e3, np.float32(3e38), -80.5, -1e3, 0.0], np.float32)
+    o2 = np.array([1.5, -2.0, 3.0, 4.0, -5.0, 6.0], np.float32)
+    np.testing.assert_array_equal(O.gate_mul(o2, z2), np.array([1.5, -2.0, 3.0, 0.0, -0.0, 3.0], np.float32))
+
+
+def _prep_inputs(rng, n_heads, n_kv, hd, rot, gated, pos):
+    qg = rng.standard_normal((n_heads, (2 if gated else 1) * hd)).astype(np.float32) * 3
+    kraw = rng.standard_normal((n_kv, hd)).astype(np.float32) * 3
+    vraw = rng.standard_normal((n_kv, hd)).astype(np.float32)
+    qnw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    knw = (0.1 * rng.standard_normal(hd)).astype(np.float32)
+    i = np.arange(rot // 2)
+    ang = pos / np.power(1e7, 2.0 * i / rot)
+    tab = np.concatenate([np.cos(ang), np.sin(ang)]).astype(np.float32)
+    return qg, kraw, vraw, qnw, knw, tab
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("zc", [False, True])
+def test_prep_norm_vs_reference_rms_norm(zc):
+    """Head norm without RoPE (identity table): the reference's cpu::rms_norm with w, or
+    with 1 + w for the zero-centred form (nx_rms_norm_add_one is rms_norm with 1 + w)."""
+    rng = np.random.default_rng(5)
+    n_heads, n_kv, hd, rot = 4, 2, 128, 32
+    qg, kraw, vraw, qnw, knw, _ = _prep_inputs(rng, n_heads, n_kv, hd, rot, False, 0)
+    tab = np.concatenate([np.ones(rot // 2), np.zeros(rot // 2)]).astype(np.float32)
+    flags = O.PREP_NO_GATE | (O.PREP_Q_ZC | O.PREP_K_ZC if zc else 0)
+    q_out, _, _, _, kv_out = O.decode_prep(qg, kraw, vraw, qnw, knw, tab, n_heads=n_heads, n_kv=n_kv, hd=hd,
+                                           rot=rot, flags=flags, eps=1e-6, pos=0, cap=1)
+    for h in range(n_heads):
+        ref = O.ref_rms_norm(qg[h], qnw + 1 if zc else qnw, 1e-6)
+        np.testing.assert_allclose(q_out[h], ref, rtol=2e-6, atol=1e-7)
+    for h in range(n_kv):
+        np.testing.assert_allclose(kv_out[0, h], O.ref_rms_norm(kraw[h], knw + 1 if zc else knw, 1e-6),
+                                   rtol=2e-6, atol=1e-7)
+        np.testing.assert_array_equal(kv_out[1, h], vraw[h])          # V: no norm, no RoPE
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("layout", [0, 1])
+def test_prep_rope_vs_reference_rope_apply(layout):
+    """Full-width RoPE with the standard angles (base 1e4): the reference's own rope_apply,
+    interleaved (layout 0) and rotate_half (layout 1).  The reference takes cos/sin of a float
+    angle near 777 rad in float; the table here rounds the double value, so a few ulp of |x| differ."""
+    rng = np.random.default_rng(6)
+    hd, pos, base = 64, 777, 10000.0
+    x = rng.standard_normal((1, hd)).astype(np.float32)
+    i = np.arange(hd // 2)
+    theta = (np.float32(pos) * (np.float32(1) / np.power(np.float32(base), (2 * i).astype(np.float32) / np.float32(hd))))
+    tab = np.concatenate([np.cos(theta.astype(np.float64)), np.sin(theta.astype(np.float64))]).astype(np.float32)
+    flags = O.PREP_NO_GATE | O.PREP_NO_QNORM | O.PREP_NO_KNORM | (O.PREP_INTERLEAVED if layout == 0 else 0)
+    q_out, *_ = O.decode_prep(x, x, x, None, None, tab, n_heads=1, n_kv=1, hd=hd, rot=hd, flags=flags,
+                              eps=1e-6, pos=pos, cap=1)
+    np.testing.assert_allclose(q_out[0], O.ref_rope(x[0], pos, hd, base, layout), rtol=0, atol=6e-5)
+
+
+def test_prep_rope_invariants():
+    """Pair norms are preserved, the unrotated tail is untouched, rotating by a then b equals
+    rotating by a+b, and rotate_half equals interleaved under the pair permutation."""
+    rng = np.random.default_rng(7)
+    n_heads, hd, rot = 3, 128, 32
+    x = rng.standard_normal((n_heads, hd)).astype(np.float32)
+    a, b = rng.uniform(-3, 3, rot // 2), rng.uniform(-3, 3, rot // 2)
+    t = lambda ang: np.concatenate([np.cos(ang), np.sin(ang)]).astype(np.float32)
+    base = dict(n_heads=n_heads, n_kv=1, hd=hd, rot=rot, eps=1e-6, pos=0, cap=1)
+    kv = np.zeros((1, hd), np.float32)
+    f = O.PREP_NO_GATE | O.PREP_NO_QNORM | O.PREP_NO_KNORM
+    ya = O.decode_prep(x, kv, kv, None, None, t(a), flags=f, **base)[0]
+    yab = O.decode_prep(ya, kv, kv, None, None, t(b), flags=f, **base)[0]
+    y = O.decode_prep(x, kv, kv, None, None, t(a + b), flags=f, **base)[0]
+    np.testing.assert_allclose(yab, y, atol=3e-5)
+    half = rot // 2
+    np.testing.assert_allclose(ya[:, :half] ** 2 + ya[:, half:rot] ** 2, x[:, :half] ** 2 + x[:, half:rot] ** 2, rtol=1e-5)
+    np.testing.assert_array_equal(ya[:, rot:], x[:, rot:])
+    perm = np.empty(rot, np.int64)
+    perm[0::2], perm[1::2] = np.arange(half), np.arange(half) + half     # interleaved slot -> half-split slot
+    xi = x.copy()
+    xi[:, :rot] = x[:, perm]
+    yi = O.decode_prep(xi, kv, kv, None, None, t(a), flags=f | O.PREP_INTERLEAVED, **base)[0]
+    np.testing.assert_allclose(yi[:, :rot], ya[:, perm], atol=1e-6)
+
+
+def test_prep_layout_gate_and_store():
+    """Gated layout: q from the first half of each head row, the raw gate from the second;
+    K/V land in row `pos` of [n_kv][cap][hd] with the chosen f16 conversion, other rows
+    untouched; kv_out holds the f32 values that were stored."""
+    rng = np.random.default_rng(8)
+    n_heads, n_kv, hd, rot, pos, cap = 4, 2, 64, 16, 5, 9
+    qg, kraw, vraw, qnw, knw, tab = _prep_inputs(rng, n_heads, n_kv, hd, rot, True, pos)
+    kc0 = rng.integers(0, 1 << 16, (n_kv, cap, hd), dtype=np.uint16)
+    vc0 = rng.integers(0, 1 << 16, (n_kv, cap, hd), dtype=np.uint16)
+    for rne in (False, True):
+        q_out, gate_out, kc, vc, kv_out = O.decode_prep(qg, kraw, vraw, qnw, knw, tab, n_heads=n_heads, n_kv=n_kv,
+                                                        hd=hd, rot=rot, flags=0, eps=1e-6, pos=pos, cap=cap,
+                                                        kc=kc0, vc=vc0, rne=rne)
+        np.testing.assert_array_equal(gate_out, qg[:, hd:])
+        plain = O.decode_prep(qg[:, :hd], kraw, vraw, qnw, knw, tab, n_heads=n_heads, n_kv=n_kv, hd=hd, rot=rot,
+                              flags=O.PREP_NO_GATE, eps=1e-6, pos=pos, cap=cap, rne=rne)
+        np.testing.assert_array_equal(q_out, plain[0])
+        conv = O.oracle().nx_f32_to_f16_rne_n if rne else O.oracle().nx_f32_to_f16_trunc_n
+        for which, cache, c0 in ((0, kc, kc0), (1, vc, vc0)):
+            want = np.zeros(n_kv * hd, np.uint16)
+            conv(np.ascontiguousarray(kv_out[which].reshape(-1)), want, want.size)
+            np.testing.assert_array_equal(cache[:, pos], want.reshape(n_kv, hd))
+            keep = np.ones(cap, bool)
+            keep[pos] = False
+            np.testing.assert_array_equal(cache[:, keep], c0[:, keep])
