@@ -129,6 +129,57 @@ int nexus_hip_attn_decode_gated(const nexus_attn_desc* desc,
                                 float* partial_ws, int n_splits,
                                 nexus_stream_t stream);
 
+/* Decode prep for one token, the step before the decode call in the gated (and plain)
+ * full-attention layers: per-head RMSNorm of q and k, RoPE over the first rot_dims dims
+ * from a host cos/sin table, the f16 store of K and V into row `pos` of the device cache,
+ * and an f32 echo of the stored K/V for the host cache.  Replaces
+ * qwen35_attn_prep.comp:1-101 as dispatched by q35_full_layer
+ * (src/gpu/vulkan_backend.h:5446-5460); the descriptor carries that shader's push
+ * constants {n_heads, n_kv, hd, rot, pos, cap, flags, eps}.
+ * Layouts (device, f32 unless noted):
+ *   qg        [n_heads][2*head_dim] per head q | gate; [n_heads][head_dim] with NO_GATE
+ *   k_raw, v_raw [n_kv_heads][head_dim]
+ *   q_norm_w, k_norm_w [head_dim] (read only when that norm is on)
+ *   rope_tab  [rot_dims]: cos(theta_i) for i < rot_dims/2, then sin(theta_i)
+ *   q_out     [n_heads][head_dim] normed + roped q;  gate_out [n_heads][head_dim] raw gate
+ *   k_cache, v_cache [n_kv_heads][cap][head_dim] f16 bits: row `pos` written
+ *   kv_out    [2][n_kv_heads][head_dim]: K then V as stored (before the f16 rounding)
+ * Norm: x * inv * (1 + w) with the ADD_ONE flag (nx_rms_norm_add_one,
+ * src/model/transformer.h:504-520), else (x * w) * inv (cpu::rms_norm,
+ * src/cpu/matmul.h:1860-1880), inv = 1/sqrt(mean(x^2) + eps).  RoPE pairs (i, i + rot/2),
+ * or (2i, 2i+1) with ROPE_INTERLEAVED (rope_apply, src/model/attention.h:593-608).
+ * f16 store: round to nearest even like the shader's packHalf2x16, or, with TRUNC_STORE,
+ * the host cache's own truncating conversion (KVCache::store, src/model/kvcache.h:903-911)
+ * so a device mirror stays bit-identical to the host cache. */
+enum nexus_prep_flags {
+    NEXUS_PREP_Q_NORM_ADD_ONE   = 1,
+    NEXUS_PREP_K_NORM_ADD_ONE   = 2,
+    NEXUS_PREP_NO_GATE          = 4,
+    NEXUS_PREP_NO_Q_NORM        = 8,
+    NEXUS_PREP_NO_K_NORM        = 16,
+    NEXUS_PREP_ROPE_INTERLEAVED = 32,
+    NEXUS_PREP_TRUNC_STORE      = 64    /* no counterpart in the shader (see above) */
+};
+
+typedef struct nexus_attn_prep_desc {
+    int32_t n_heads;         /* q heads (> 0)                                  */
+    int32_t n_kv_heads;      /* k/v heads (> 0)                                */
+    int32_t head_dim;        /* 1..512 (the shader's limit)                    */
+    int32_t rot_dims;        /* even, 0..head_dim                              */
+    int32_t pos;             /* cache row written, 0 <= pos < cap              */
+    int32_t flags;           /* enum nexus_prep_flags                          */
+    int64_t cap;             /* rows per kv head in k_cache / v_cache          */
+    float   eps;             /* RMSNorm epsilon (>= 0)                         */
+    int32_t reserved;        /* 0                                              */
+} nexus_attn_prep_desc;
+
+int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* desc,
+                               const float* qg, const float* k_raw, const float* v_raw,
+                               const float* q_norm_w, const float* k_norm_w, const float* rope_tab,
+                               float* q_out, float* gate_out,
+                               uint16_t* k_cache, uint16_t* v_cache, float* kv_out,
+                               nexus_stream_t stream);
+
 /* Message for the last non-zero status on the calling thread ("" if none). */
 const char* nexus_hip_attn_last_error(void);
 /* Library version, e.g. "nexus_hip_attn 0.1.0 gfx950". */

@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "nexus_hip_attn_decode_default_splits",
     "nexus_hip_attn_prefill_gated",
     "nexus_hip_attn_decode_gated",
+    "nexus_hip_attn_decode_prep",
     "nexus_hip_attn_last_error",
     "nexus_hip_attn_version",
 )
@@ -63,6 +64,32 @@ def make_desc(*, n_q_heads: int, n_kv_heads: int, head_dim: int, n_query: int, q
     return AttnDesc(n_q_heads, n_kv_heads, head_dim, n_query, q_base_pos, n_ctx,
                     n_ctx if kv_row_stride is None else kv_row_stride, sliding_window,
                     scale, softcap, q_dtype, o_dtype)
+
+
+# enum nexus_prep_flags
+PREP_Q_NORM_ADD_ONE = 1
+PREP_K_NORM_ADD_ONE = 2
+PREP_NO_GATE = 4
+PREP_NO_Q_NORM = 8
+PREP_NO_K_NORM = 16
+PREP_ROPE_INTERLEAVED = 32
+PREP_TRUNC_STORE = 64
+
+
+class PrepDesc(ctypes.Structure):
+    """struct nexus_attn_prep_desc (include/nexus_hip_attn.h)."""
+
+    _fields_ = [
+        ("n_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rot_dims", ctypes.c_int32),
+        ("pos", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("cap", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
 
 
 class NexusAttnError(RuntimeError):
@@ -100,6 +127,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.nexus_hip_attn_prefill_gated.restype = ctypes.c_int
     lib.nexus_hip_attn_decode_gated.argtypes = [dp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
     lib.nexus_hip_attn_decode_gated.restype = ctypes.c_int
+    lib.nexus_hip_attn_decode_prep.argtypes = [ctypes.POINTER(PrepDesc)] + [vp] * 12
+    lib.nexus_hip_attn_decode_prep.restype = ctypes.c_int
     lib.nexus_hip_attn_last_error.argtypes = []
     lib.nexus_hip_attn_last_error.restype = ctypes.c_char_p
     lib.nexus_hip_attn_version.argtypes = []
@@ -155,6 +184,14 @@ def decode_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, ws: int, n_spli
     return _check(rc) if check else rc
 
 
+def decode_prep_raw(desc: PrepDesc, qg: int, k_raw: int, v_raw: int, q_norm_w: int, k_norm_w: int,
+                    rope_tab: int, q_out: int, gate_out: int, k_cache: int, v_cache: int, kv_out: int,
+                    stream: int, check: bool = True) -> int:
+    rc = load().nexus_hip_attn_decode_prep(ctypes.byref(desc), qg, k_raw, v_raw, q_norm_w, k_norm_w, rope_tab,
+                                           q_out, gate_out, k_cache, v_cache, kv_out, stream)
+    return _check(rc) if check else rc
+
+
 def prefill_flops(n_q_heads: int, head_dim: int, n_query: int, q_base_pos: int, n_ctx: int,
                   sliding_window: int = 0) -> float:
     """Algorithmic FLOPs of a causal prefill: 4*hd per visible (query, key) pair per head."""
@@ -172,6 +209,18 @@ def decode_bytes(n_kv_heads: int, head_dim: int, n_keys: int, n_q_heads: int, n_
     """Algorithmic HBM bytes of a decode: K and V of every visible key once, plus Q and O."""
     return (2.0 * n_kv_heads * n_keys * head_dim * 2
             + n_query * n_q_heads * head_dim * (q_bytes + o_bytes))
+
+
+def decode_prep_bytes(n_heads: int, n_kv_heads: int, head_dim: int, gated: bool, q_norm: bool,
+                      k_norm: bool, rot_dims: int) -> float:
+    """Algorithmic HBM bytes of one decode prep: every input read once, every output written
+    once (q/gate/k/v in f32, the two f16 cache rows, the f32 K/V echo, weights and table)."""
+    q_in = n_heads * head_dim * 4 * (2 if gated else 1)
+    kv_in = 2 * n_kv_heads * head_dim * 4
+    w = head_dim * 4 * (int(q_norm) + int(k_norm)) + rot_dims * 4
+    q_out = n_heads * head_dim * 4 * (2 if gated else 1)
+    kv_out = 2 * n_kv_heads * head_dim * (2 + 4)
+    return float(q_in + kv_in + w + q_out + kv_out)
 
 
 def default_scale(head_dim: int) -> float:

@@ -318,6 +318,62 @@ int nexus_hip_attn_decode(const nexus_attn_desc* desc, const void* q, const uint
     return nexus_hip_attn_decode_gated(desc, q, k, v, nullptr, out, partial_ws, n_splits, stream);
 }
 
+static_assert(NEXUS_PREP_Q_NORM_ADD_ONE == nxa::kPrepQZeroCentred && NEXUS_PREP_K_NORM_ADD_ONE == nxa::kPrepKZeroCentred &&
+                  NEXUS_PREP_NO_GATE == nxa::kPrepNoGate && NEXUS_PREP_NO_Q_NORM == nxa::kPrepNoQNorm &&
+                  NEXUS_PREP_NO_K_NORM == nxa::kPrepNoKNorm && NEXUS_PREP_ROPE_INTERLEAVED == nxa::kPrepInterleaved &&
+                  NEXUS_PREP_TRUNC_STORE == nxa::kPrepTruncStore,
+              "prep flag bits of the C ABI and the kernel differ");
+
+int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, const float* k_raw,
+                               const float* v_raw, const float* q_norm_w, const float* k_norm_w,
+                               const float* rope_tab, float* q_out, float* gate_out, uint16_t* k_cache,
+                               uint16_t* v_cache, float* kv_out, nexus_stream_t stream)
+{
+    if (!d) return fail(NEXUS_E_INVALID, "desc is NULL");
+    if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_heads > 65536 || d->n_kv_heads > 65536)
+        return fail(NEXUS_E_INVALID, "n_heads=%d n_kv_heads=%d", d->n_heads, d->n_kv_heads);
+    if (d->head_dim <= 0 || d->head_dim > nxa::kPrepMaxHeadDim)
+        return fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in [1, %d]", d->head_dim, nxa::kPrepMaxHeadDim);
+    if (d->rot_dims < 0 || d->rot_dims > d->head_dim || (d->rot_dims & 1))
+        return fail(NEXUS_E_INVALID, "rot_dims=%d must be even and in [0, head_dim=%d]", d->rot_dims, d->head_dim);
+    if (d->cap <= 0 || d->pos < 0 || d->pos >= d->cap)
+        return fail(NEXUS_E_INVALID, "pos=%d outside the cache rows [0, cap=%lld)", d->pos, (long long)d->cap);
+    if (d->flags & ~127) return fail(NEXUS_E_INVALID, "unknown flag bits 0x%x", d->flags & ~127);
+    if (!(d->eps >= 0.f) || !std::isfinite(d->eps)) return fail(NEXUS_E_INVALID, "eps=%g", (double)d->eps);
+    if (d->reserved != 0) return fail(NEXUS_E_INVALID, "reserved=%d must be 0", d->reserved);
+    const bool gated = (d->flags & NEXUS_PREP_NO_GATE) == 0;
+    if (!qg || !k_raw || !v_raw || !q_out || !k_cache || !v_cache || !kv_out)
+        return fail(NEXUS_E_INVALID, "null qg/k_raw/v_raw/q_out/k_cache/v_cache/kv_out pointer");
+    if (gated && !gate_out) return fail(NEXUS_E_INVALID, "gate_out is NULL for a gated layer");
+    if (!(d->flags & NEXUS_PREP_NO_Q_NORM) && !q_norm_w) return fail(NEXUS_E_INVALID, "q_norm_w is NULL");
+    if (!(d->flags & NEXUS_PREP_NO_K_NORM) && !k_norm_w) return fail(NEXUS_E_INVALID, "k_norm_w is NULL");
+    if (d->rot_dims > 0 && !rope_tab) return fail(NEXUS_E_INVALID, "rope_tab is NULL");
+
+    nxa::PrepArgs a{};
+    a.qg = qg;
+    a.kraw = k_raw;
+    a.vraw = v_raw;
+    a.qnw = q_norm_w;
+    a.knw = k_norm_w;
+    a.tab = rope_tab;
+    a.q_out = q_out;
+    a.gate_out = gate_out;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.kv_out = kv_out;
+    a.cap = d->cap;
+    a.n_heads = d->n_heads;
+    a.n_kv = d->n_kv_heads;
+    a.hd = d->head_dim;
+    a.rot = d->rot_dims;
+    a.pos = d->pos;
+    a.flags = d->flags;
+    a.eps = d->eps;
+    const hipError_t e = nxa::launch_decode_prep(a, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode prep launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
 size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
 {
     if (check_desc(desc) != NEXUS_OK) return 0;

@@ -66,6 +66,34 @@ struct CombineArgs {
     int n_rows, n_splits;
 };
 
+// Decode prep (attn_prep.hip): flag bits of qwen35_attn_prep.comp:7-8, plus a truncating
+// store that matches the host cache's own conversion (KVCache::store, kvcache.h:903-911).
+constexpr int kPrepMaxHeadDim = 512;
+constexpr int kPrepQZeroCentred = 1;
+constexpr int kPrepKZeroCentred = 2;
+constexpr int kPrepNoGate = 4;
+constexpr int kPrepNoQNorm = 8;
+constexpr int kPrepNoKNorm = 16;
+constexpr int kPrepInterleaved = 32;
+constexpr int kPrepTruncStore = 64;
+
+struct PrepArgs {
+    const float* qg;                // [n_heads][2*hd] (q | gate) or [n_heads][hd] without gate
+    const float* kraw;              // [n_kv][hd]
+    const float* vraw;              // [n_kv][hd]
+    const float* qnw;               // [hd] q norm weight (read only when the q norm is on)
+    const float* knw;               // [hd]
+    const float* tab;               // [rot]: cos[rot/2] then sin[rot/2]
+    float* q_out;                   // [n_heads][hd]
+    float* gate_out;                // [n_heads][hd] (gated layers)
+    uint16_t* kc;                   // [n_kv][cap][hd] f16
+    uint16_t* vc;
+    float* kv_out;                  // [2][n_kv][hd]: K then V as stored
+    long long cap;
+    int n_heads, n_kv, hd, rot, pos, flags;
+    float eps;
+};
+
 // Workspace = f32 partials [rows][splits][hd+2], the reference's split-K partial format
 // (qwen35_attn_part.comp:3).  It carries no state between calls.
 inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
@@ -85,5 +113,7 @@ hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool 
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);
 hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream);
+// One workgroup (one wave) per q, k and v head: n_heads + 2 * n_kv workgroups.
+hipError_t launch_decode_prep(const PrepArgs& a, hipStream_t stream);
 
 }  // namespace nxa

@@ -108,3 +108,48 @@ def attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads
     capi.decode_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                     partial_ws.data_ptr(), n_splits, stream, gate=gate_ptr)
     return out
+
+
+def decode_prep(qg: torch.Tensor, k_raw: torch.Tensor, v_raw: torch.Tensor, k_cache: torch.Tensor,
+                v_cache: torch.Tensor, *, pos: int, rope_tab: torch.Tensor | None,
+                q_norm_w: torch.Tensor | None = None, k_norm_w: torch.Tensor | None = None,
+                gated: bool = True, q_norm_add_one: bool = False, k_norm_add_one: bool = False,
+                rope_interleaved: bool = False, eps: float = 1e-6, trunc_store: bool = False,
+                q_out: torch.Tensor | None = None, gate_out: torch.Tensor | None = None,
+                kv_out: torch.Tensor | None = None):
+    """One token's decode prep (nexus_hip_attn_decode_prep): q/k head norms (a weight of None
+    turns that norm off), RoPE over rope_tab.numel() dims, K/V stored into row `pos` of
+    k_cache/v_cache [n_kv, cap, hd] (f16).  qg is [n_heads, 2*hd] (q | gate) when gated,
+    else [n_heads, hd]; k_raw/v_raw [n_kv, hd]; all f32.  Returns (q_out [n_heads, hd],
+    gate_out [n_heads, hd] or None, kv_out [2, n_kv, hd])."""
+    n_kv, cap, hd = k_cache.shape
+    n_heads = qg.shape[0]
+    f32 = [("qg", qg), ("k_raw", k_raw), ("v_raw", v_raw)]
+    f32 += [(n, t) for n, t in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w), ("rope_tab", rope_tab)) if t is not None]
+    for name, t in f32 + [("k_cache", k_cache), ("v_cache", v_cache)]:
+        if not t.is_cuda or not t.is_contiguous():
+            raise RuntimeError(f"{name} must be a contiguous device tensor (no CPU path)")
+    for name, t in f32:
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32, got {t.dtype}")
+    _kv_view(k_cache), _kv_view(v_cache)
+    if qg.shape != (n_heads, (2 if gated else 1) * hd) or k_raw.shape != (n_kv, hd) or v_raw.shape != (n_kv, hd):
+        raise ValueError(f"qg {tuple(qg.shape)} / k_raw {tuple(k_raw.shape)} do not match n_kv={n_kv} hd={hd}")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache differ in shape")
+    flags = ((capi.PREP_Q_NORM_ADD_ONE if q_norm_add_one else 0) | (capi.PREP_K_NORM_ADD_ONE if k_norm_add_one else 0)
+             | (0 if gated else capi.PREP_NO_GATE) | (capi.PREP_NO_Q_NORM if q_norm_w is None else 0)
+             | (capi.PREP_NO_K_NORM if k_norm_w is None else 0)
+             | (capi.PREP_ROPE_INTERLEAVED if rope_interleaved else 0) | (capi.PREP_TRUNC_STORE if trunc_store else 0))
+    rot = 0 if rope_tab is None else rope_tab.numel()
+    desc = capi.PrepDesc(n_heads, n_kv, hd, rot, pos, flags, cap, eps, 0)
+    dev = qg.device
+    q_out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev) if q_out is None else q_out
+    if gated and gate_out is None:
+        gate_out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev)
+    kv_out = torch.empty(2, n_kv, hd, dtype=torch.float32, device=dev) if kv_out is None else kv_out
+    ptr = lambda t: 0 if t is None else t.data_ptr()
+    capi.decode_prep_raw(desc, qg.data_ptr(), k_raw.data_ptr(), v_raw.data_ptr(), ptr(q_norm_w), ptr(k_norm_w),
+                         ptr(rope_tab), q_out.data_ptr(), ptr(gate_out if gated else None), k_cache.data_ptr(),
+                         v_cache.data_ptr(), kv_out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+    return q_out, (gate_out if gated else None), kv_out

@@ -29,25 +29,33 @@ def test_library_exports_every_declared_symbol():
     assert "gfx950" in capi.version()
 
 
-def test_desc_layout_matches_header(tmp_path):
-    """The ctypes mirror of nexus_attn_desc has the C compiler's size and offsets."""
+@pytest.mark.parametrize("cls,cname", [(capi.AttnDesc, "nexus_attn_desc"), (capi.PrepDesc, "nexus_attn_prep_desc")])
+def test_desc_layout_matches_header(tmp_path, cls, cname):
+    """The ctypes mirrors of the descriptors have the C compiler's size and offsets."""
     import shutil
     import subprocess
 
     cc = shutil.which("gcc") or shutil.which("cc")
     if cc is None:
         pytest.skip("no C compiler on this host")
-    fields = [f[0] for f in capi.AttnDesc._fields_]
+    fields = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "nexus_hip_attn.h"\nint main(void){'
-                   'printf("%zu", sizeof(nexus_attn_desc));'
-                   + "".join(f'printf(" %zu", offsetof(nexus_attn_desc, {f}));' for f in fields)
+                   f'printf("%zu", sizeof({cname}));'
+                   + "".join(f'printf(" %zu", offsetof({cname}, {f}));' for f in fields)
                    + "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run([cc, f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    assert got[0] == ctypes.sizeof(capi.AttnDesc)
-    assert got[1:] == [getattr(capi.AttnDesc, f).offset for f in fields]
+    assert got[0] == ctypes.sizeof(cls)
+    assert got[1:] == [getattr(cls, f).offset for f in fields]
+
+
+def test_prep_flag_values_match_header():
+    text = HEADER.read_text()
+    for name in ("Q_NORM_ADD_ONE", "K_NORM_ADD_ONE", "NO_GATE", "NO_Q_NORM", "NO_K_NORM", "ROPE_INTERLEAVED", "TRUNC_STORE"):
+        m = re.search(rf"NEXUS_PREP_{name}\s*=\s*(\d+)", text)
+        assert m and int(m.group(1)) == getattr(capi, f"PREP_{name}"), name
 
 
 def _desc(**kw):
@@ -118,3 +126,48 @@ def test_algorithmic_work_formulas():
     assert capi.prefill_flops(40, 128, 512, 4096, 4608) == 4 * 128 * 40 * 2_228_480
     assert capi.prefill_flops(40, 128, 8192, 0, 8192) == 4 * 128 * 40 * 33_558_528
     assert capi.decode_bytes(8, 128, 61440, 40, 1) == 2 * 8 * 61440 * 128 * 2 + 40 * 128 * 8
+
+
+def _prep_desc(**kw):
+    base = dict(n_heads=8, n_kv_heads=2, head_dim=128, rot_dims=32, pos=5, flags=0, cap=16, eps=1e-6, reserved=0)
+    base.update(kw)
+    return capi.PrepDesc(**base)
+
+
+PREP_BAD = [
+    (dict(n_heads=0), capi.NEXUS_E_INVALID),
+    (dict(n_kv_heads=-1), capi.NEXUS_E_INVALID),
+    (dict(head_dim=0), capi.NEXUS_E_UNSUPPORTED),
+    (dict(head_dim=520, rot_dims=0), capi.NEXUS_E_UNSUPPORTED),
+    (dict(rot_dims=31), capi.NEXUS_E_INVALID),
+    (dict(rot_dims=130), capi.NEXUS_E_INVALID),
+    (dict(pos=16), capi.NEXUS_E_INVALID),
+    (dict(pos=-1), capi.NEXUS_E_INVALID),
+    (dict(cap=0, pos=0), capi.NEXUS_E_INVALID),
+    (dict(flags=128), capi.NEXUS_E_INVALID),
+    (dict(eps=float("inf")), capi.NEXUS_E_INVALID),
+    (dict(reserved=1), capi.NEXUS_E_INVALID),
+]
+
+
+@pytest.mark.parametrize("kw,code", PREP_BAD)
+def test_prep_declines_before_side_effects(kw, code):
+    out = np.full(64, 7.0, np.float32)
+    p, o = np.zeros(64, np.float32).ctypes.data, out.ctypes.data
+    rc = capi.decode_prep_raw(_prep_desc(**kw), p, p, p, p, p, p, o, o, o, o, o, 0, check=False)
+    assert rc == code, capi.last_error()
+    assert capi.last_error()
+    assert np.all(out == 7.0)
+
+
+def test_prep_null_pointers_declined():
+    """Pointers are required exactly where the flags say the kernel reads or writes them."""
+    out = np.full(64, 7.0, np.float32)
+    p, o = np.zeros(64, np.float32).ctypes.data, out.ctypes.data
+    d = _prep_desc()
+    assert capi.decode_prep_raw(d, p, p, p, p, p, p, o, 0, o, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # gate_out
+    assert capi.decode_prep_raw(d, p, p, p, 0, p, p, o, o, o, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # q norm w
+    assert capi.decode_prep_raw(d, p, p, p, p, 0, p, o, o, o, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # k norm w
+    assert capi.decode_prep_raw(d, p, p, p, p, p, 0, o, o, o, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # table
+    assert capi.decode_prep_raw(d, p, p, p, p, p, p, o, o, 0, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # k cache
+    assert np.all(out == 7.0)
