@@ -4,9 +4,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <set>
 #include <string>
 
@@ -52,8 +54,13 @@ HipAttnBackend::~HipAttnBackend()
 {
     if (!ready_) return;
     (void)hipSetDevice(device_);
-    for (DevBuf* b : {&q_, &k_, &v_, &o_, &ws_})
+    (void)hipDeviceSynchronize();
+    for (DevBuf* b : {&q_, &k_, &v_, &o_, &ws_, &prep_q_, &prep_gate_, &prep_kv_, &prep_par_})
         if (b->ptr) (void)hipFree(b->ptr);
+    for (auto& m : mirrors_) {
+        if (m.second.k.ptr) (void)hipFree(m.second.k.ptr);
+        if (m.second.v.ptr) (void)hipFree(m.second.v.ptr);
+    }
     if (stream_) (void)hipStreamDestroy((hipStream_t)stream_);
 }
 
@@ -88,8 +95,8 @@ bool HipAttnBackend::ensure(DevBuf& b, size_t bytes, bool zero)
     if (bytes == 0) bytes = 256;
     if (b.ptr && b.bytes >= bytes) return true;
     if (b.ptr) {
-        // the stream may still read the old buffer
-        if (hipStreamSynchronize((hipStream_t)stream_) != hipSuccess) return false;
+        // work in flight on any stream (the caller's too) may still read the old buffer
+        if (hipDeviceSynchronize() != hipSuccess) return false;
         (void)hipFree(b.ptr);
         b = DevBuf{};
     }
@@ -230,6 +237,303 @@ bool HipAttnBackend::decode_device(const nexus_attn_desc& d, const void* q, cons
     std::lock_guard<std::mutex> l(mu_);
     if (!ready_) return decline("no HIP device (HipAttnBackend::init not called or failed)");
     return run_device(d, q, k, v, out, n_splits, /*decode=*/true, (void*)stream);
+}
+
+// ------------------------------------------------------------------ device KV mirror
+
+bool HipAttnBackend::alloc_exact(DevBuf& b, size_t bytes)
+{
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    b.ptr = p;
+    b.bytes = bytes;
+    return true;
+}
+
+void HipAttnBackend::free_buf(DevBuf& b)
+{
+    if (b.ptr) (void)hipFree(b.ptr);
+    b = DevBuf{};
+}
+
+void HipAttnBackend::drop_locked(const void* owner, int layer)
+{
+    bool synced = false;
+    for (auto it = mirrors_.begin(); it != mirrors_.end();) {
+        if (it->first.first == owner && (layer < 0 || it->first.second == layer)) {
+            if (!synced) {                               // kernels in flight may still read it
+                (void)hipDeviceSynchronize();
+                synced = true;
+            }
+            kv_mirror_used_ -= std::min(kv_mirror_used_, it->second.bytes);
+            free_buf(it->second.k);
+            free_buf(it->second.v);
+            it = mirrors_.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
+void HipAttnBackend::q35_kv_drop(const void* owner, int layer)
+{
+    std::lock_guard<std::mutex> l(mu_);
+    if (!ready_) return;
+    (void)hipSetDevice(device_);
+    drop_locked(owner, layer);
+}
+
+void HipAttnBackend::set_gpu_kv_mb(int mb)
+{
+    std::lock_guard<std::mutex> l(mu_);
+    gpu_kv_mb_ = mb < 0 ? -1 : mb;
+}
+
+int HipAttnBackend::gpu_kv_mb()
+{
+    if (gpu_kv_mb_ == -2) {                              // vulkan_backend.h:5277-5284
+        gpu_kv_mb_ = -1;
+        if (const char* e = std::getenv("NEXUS_GPU_KV")) {
+            if (!std::strcmp(e, "off") || !std::strcmp(e, "0")) gpu_kv_mb_ = 0;
+            else if (std::strcmp(e, "auto") && *e) {
+                const int v = std::atoi(e);
+                gpu_kv_mb_ = v > 0 ? v : -1;
+            }
+        }
+    }
+    return gpu_kv_mb_;
+}
+
+size_t HipAttnBackend::kv_mirror_cap_bytes()
+{
+    const int mb = gpu_kv_mb();
+    if (mb == 0 || !ready_) return 0;
+    if (mb > 0) return (size_t)mb << 20;
+    // auto (vulkan_backend.h:5192-5205, with the runtime's free-memory figure in place of
+    // the reference's weight bookkeeping): what is free now plus the mirrors' own bytes.
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    const size_t avail = free_b + kv_mirror_used_;
+    const size_t margin = std::max<size_t>(768ull << 20, total_b / 5) + (64ull << 20);
+    return avail > margin ? avail - margin : 0;
+}
+
+bool HipAttnBackend::kv_mirror_info(const void* owner, int layer, size_t* cap, size_t* valid)
+{
+    std::lock_guard<std::mutex> l(mu_);
+    auto it = mirrors_.find({owner, layer});
+    if (it == mirrors_.end() || it->second.cap == 0) return false;
+    if (cap) *cap = it->second.cap;
+    if (valid) *valid = it->second.valid;
+    return true;
+}
+
+bool HipAttnBackend::kv_mirror_read(const void* owner, int layer, int kv_head, int pos0, int n, uint16_t* k_out,
+                                    uint16_t* v_out)
+{
+    std::lock_guard<std::mutex> l(mu_);
+    auto it = mirrors_.find({owner, layer});
+    if (it == mirrors_.end() || it->second.cap == 0 || !k_out || !v_out) return false;
+    const KvMirror& m = it->second;
+    if (kv_head < 0 || (uint32_t)kv_head >= m.n_kv || pos0 < 0 || n < 0 || (size_t)pos0 + (size_t)n > m.cap)
+        return false;
+    (void)hipSetDevice(device_);
+    const size_t row = (size_t)m.hd * sizeof(uint16_t);
+    const size_t off = ((size_t)kv_head * m.cap + (size_t)pos0) * row;
+    hipStream_t s = (hipStream_t)stream_;
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpyAsync(k_out, (const char*)m.k.ptr + off, (size_t)n * row, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipMemcpyAsync(v_out, (const char*)m.v.ptr + off, (size_t)n * row, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return false;
+    return true;
+}
+
+bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const float* k_raw, const float* v_raw,
+                                   float* attn_out, float* kv_out_host, uint32_t* mirror_valid_out,
+                                   nexus_stream_t stream)
+{
+    std::lock_guard<std::mutex> l(mu_);
+    if (!ready_) return decline("no HIP device (HipAttnBackend::init not called or failed)");
+    if (!qg || !k_raw || !v_raw || !attn_out || !kv_out_host) return decline("q35_attention: null pointer");
+    const uint32_t nh = d.n_heads, nkv = d.n_kv, hd = d.hd;
+    if (nh == 0 || nkv == 0 || nh % nkv != 0) return decline("q35_attention: n_heads must be a multiple of n_kv");
+    if (d.rot > hd || (d.rot & 1) || (d.rot > 0 && !d.rope_tab))
+        return decline("q35_attention: rot must be even, <= hd, with a table");
+    if (d.has_gate && (!d.q_norm || !d.k_norm)) return decline("q35_attention: gated layer without q/k norm");
+    if (!d.k_host || !d.v_host || d.host_tokens < d.pos) return decline("q35_attention: host cache missing or short");
+    if (d.pos >= (uint32_t)INT32_MAX - 1) return decline("q35_attention: pos beyond the 31-bit range");
+    for (uint32_t h = 0; h < nkv; ++h)
+        if (d.pos > 0 && (!d.k_host[h] || !d.v_host[h])) return decline("q35_attention: null host head");
+    const uint32_t need = d.pos + 1;
+
+    // attention over the mirror: validated before anything is allocated or copied
+    nexus_attn_desc ad{};
+    ad.n_q_heads = (int)nh;
+    ad.n_kv_heads = (int)nkv;
+    ad.head_dim = (int)hd;
+    ad.n_query = 1;
+    ad.q_base_pos = (int)d.pos;
+    ad.n_ctx = (int)need;
+    ad.kv_row_stride = need;                             // the real stride (cap >= need) is set below
+    ad.scale = d.scale;
+    ad.q_dtype = NEXUS_DT_F32;
+    ad.o_dtype = NEXUS_DT_F32;
+    const int splits = nexus_hip_attn_decode_default_splits(&ad);
+    const size_t ws_bytes = splits > 0 ? nexus_hip_attn_decode_ws_bytes(&ad, splits) : 0;
+    if (ws_bytes == 0) return decline(nexus_hip_attn_last_error());
+
+    const size_t cap_bytes = kv_mirror_cap_bytes();
+    if (cap_bytes == 0) return decline("q35_attention: GPU KV mirror is off (NEXUS_GPU_KV / set_gpu_kv_mb)");
+    if (hipSetDevice(device_) != hipSuccess) return decline("hipSetDevice failed");
+    hipStream_t s = stream ? (hipStream_t)stream : (hipStream_t)stream_;
+
+    // ---- find / grow (vulkan_backend.h:5349-5391)
+    const std::pair<const void*, int> key{d.owner, d.layer};
+    auto it = mirrors_.find(key);
+    if (it != mirrors_.end() && it->second.cap && (it->second.n_kv != nkv || it->second.hd != hd)) {
+        drop_locked(d.owner, d.layer);
+        it = mirrors_.end();
+    }
+    if (it == mirrors_.end()) it = mirrors_.emplace(key, KvMirror{}).first;
+    KvMirror& mm = it->second;
+    size_t eff_valid = std::min<size_t>(mm.valid, d.host_synced);
+    if (mm.cap < need) {
+        if (mm.refused_need && need < mm.refused_need)
+            return decline("q35_attention: the mirror was refused for a larger context recently");
+        const size_t per_tok = (size_t)nkv * hd * 2 * sizeof(uint16_t);     // K + V
+        size_t newcap = std::max<size_t>(((size_t)need * 5 / 4 + 255) & ~(size_t)255, 2048);
+        const size_t others = kv_mirror_used_ - std::min(kv_mirror_used_, mm.bytes);
+        if (others + newcap * per_tok > cap_bytes) newcap = ((size_t)need + 255) & ~(size_t)255;
+        if (others + newcap * per_tok > cap_bytes) {
+            if (mm.cap) drop_locked(d.owner, d.layer);
+            mirrors_[key].refused_need = need + 1024;
+            return decline("q35_attention: the mirror would exceed the GPU KV budget");
+        }
+        const size_t half = newcap * (size_t)nkv * hd * sizeof(uint16_t);
+        KvMirror nm;
+        bool ok = alloc_exact(nm.k, half) && alloc_exact(nm.v, half);
+        if (!ok && mm.cap) {                             // no room for both: give the old one up first
+            free_buf(nm.k);
+            free_buf(nm.v);
+            drop_locked(d.owner, d.layer);
+            it = mirrors_.emplace(key, KvMirror{}).first;
+            eff_valid = 0;
+            ok = alloc_exact(nm.k, half) && alloc_exact(nm.v, half);
+        }
+        KvMirror& cur = it->second;
+        if (!ok) {
+            free_buf(nm.k);
+            free_buf(nm.v);
+            cur.refused_need = need + 1024;
+            return decline("q35_attention: device allocation of the mirror failed");
+        }
+        if (cur.cap && eff_valid > 0) {
+            // keep the rows still in sync: one strided device copy per cache instead of a
+            // refill over PCIe (the reference reallocates and refills from the host)
+            const size_t row = (size_t)hd * sizeof(uint16_t);
+            if (hipMemcpy2DAsync(nm.k.ptr, newcap * row, cur.k.ptr, cur.cap * row, eff_valid * row, nkv,
+                                 hipMemcpyDeviceToDevice, s) != hipSuccess ||
+                hipMemcpy2DAsync(nm.v.ptr, newcap * row, cur.v.ptr, cur.cap * row, eff_valid * row, nkv,
+                                 hipMemcpyDeviceToDevice, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) {
+                (void)hipGetLastError();
+                eff_valid = 0;
+            }
+        } else {
+            eff_valid = 0;
+        }
+        if (cur.cap) (void)hipDeviceSynchronize();
+        kv_mirror_used_ -= std::min(kv_mirror_used_, cur.bytes);
+        free_buf(cur.k);
+        free_buf(cur.v);
+        nm.cap = newcap;
+        nm.bytes = newcap * per_tok;
+        nm.n_kv = nkv;
+        nm.hd = hd;
+        nm.valid = eff_valid;
+        kv_mirror_used_ += nm.bytes;
+        cur = nm;
+    }
+    KvMirror& m = it->second;
+
+    // ---- per-call device buffers (grown, never shrunk)
+    const size_t q_bytes = (size_t)nh * hd * sizeof(float), kv_bytes = 2 * (size_t)nkv * hd * sizeof(float);
+    const size_t par_floats = (size_t)d.rot + 2 * (size_t)hd;
+    if (!ensure(prep_q_, q_bytes, false) || !ensure(prep_gate_, q_bytes, false) || !ensure(prep_kv_, kv_bytes, false) ||
+        !ensure(prep_par_, par_floats * sizeof(float), false) || !ensure(ws_, ws_bytes, true))
+        return decline("q35_attention: device scratch allocation failed");
+
+    // ---- fill rows [eff_valid, pos) from the host (vulkan_backend.h:5392-5418)
+    const size_t row = (size_t)hd * sizeof(uint16_t);
+    if (eff_valid < d.pos) {
+        const size_t n = d.pos - eff_valid;
+        for (uint32_t h = 0; h < nkv; ++h) {
+            const size_t off = ((size_t)h * m.cap + eff_valid) * row;
+            if (hipMemcpyAsync((char*)m.k.ptr + off, d.k_host[h] + eff_valid * hd, n * row, hipMemcpyHostToDevice, s) !=
+                    hipSuccess ||
+                hipMemcpyAsync((char*)m.v.ptr + off, d.v_host[h] + eff_valid * hd, n * row, hipMemcpyHostToDevice, s) !=
+                    hipSuccess) {
+                m.valid = std::min(m.valid, eff_valid);
+                return decline("q35_attention: host-to-device fill failed");
+            }
+        }
+    }
+    m.valid = d.pos;
+
+    // ---- norm weights and the RoPE table: one small upload
+    float* par = (float*)prep_par_.ptr;
+    const float* tab_d = par;
+    const float* qnw_d = par + d.rot;
+    const float* knw_d = par + d.rot + hd;
+    const size_t fb = sizeof(float);
+    if ((d.rot && hipMemcpyAsync(par, d.rope_tab, d.rot * fb, hipMemcpyHostToDevice, s) != hipSuccess) ||
+        (d.q_norm && hipMemcpyAsync(par + d.rot, d.q_norm, hd * fb, hipMemcpyHostToDevice, s) != hipSuccess) ||
+        (d.k_norm && hipMemcpyAsync(par + d.rot + hd, d.k_norm, hd * fb, hipMemcpyHostToDevice, s) != hipSuccess))
+        return decline("q35_attention: parameter upload failed");
+
+    // ---- prep: head norms, RoPE, store of row `pos` (vulkan_backend.h:5446-5460)
+    nexus_attn_prep_desc pd{};
+    pd.n_heads = (int)nh;
+    pd.n_kv_heads = (int)nkv;
+    pd.head_dim = (int)hd;
+    pd.rot_dims = (int)d.rot;
+    pd.pos = (int)d.pos;
+    pd.cap = (int64_t)m.cap;
+    pd.eps = d.norm_eps;
+    pd.flags = (d.q_zc ? NEXUS_PREP_Q_NORM_ADD_ONE : 0) | (d.k_zc ? NEXUS_PREP_K_NORM_ADD_ONE : 0) |
+               (d.has_gate ? 0 : NEXUS_PREP_NO_GATE) | (d.q_norm ? 0 : NEXUS_PREP_NO_Q_NORM) |
+               (d.k_norm ? 0 : NEXUS_PREP_NO_K_NORM) | (d.rope_interleaved ? NEXUS_PREP_ROPE_INTERLEAVED : 0) |
+               (mirror_rne_ ? 0 : NEXUS_PREP_TRUNC_STORE);
+    float* q_d = (float*)prep_q_.ptr;
+    float* gate_d = (float*)prep_gate_.ptr;
+    float* kv_d = (float*)prep_kv_.ptr;
+    int rc = nexus_hip_attn_decode_prep(&pd, qg, k_raw, v_raw, d.q_norm ? qnw_d : nullptr, d.k_norm ? knw_d : nullptr,
+                                        d.rot ? tab_d : nullptr, q_d, d.has_gate ? gate_d : nullptr,
+                                        (uint16_t*)m.k.ptr, (uint16_t*)m.v.ptr, kv_d, (nexus_stream_t)s);
+    if (rc != NEXUS_OK) {
+        m.valid = std::min<size_t>(m.valid, d.pos);
+        return decline(nexus_hip_attn_last_error());
+    }
+    // ---- split-KV attention over the mirror, output gate fused into the combine
+    ad.kv_row_stride = (int64_t)m.cap;
+    rc = nexus_hip_attn_decode_gated(&ad, q_d, (const uint16_t*)m.k.ptr, (const uint16_t*)m.v.ptr,
+                                     d.has_gate ? gate_d : nullptr, attn_out, (float*)ws_.ptr, splits,
+                                     (nexus_stream_t)s);
+    if (rc != NEXUS_OK) return decline(nexus_hip_attn_last_error());
+    if (hipMemcpyAsync(kv_out_host, kv_d, kv_bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return decline("q35_attention: device-to-host copy of K/V failed");
+    m.valid = need;
+    if (mirror_valid_out) *mirror_valid_out = need;
+    ++calls_run_;
+    return true;
 }
 
 HipAttnBackend& backend()

@@ -24,7 +24,9 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "nexus_hip_attn.h"
 
@@ -91,6 +93,60 @@ public:
     bool decode_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
                        const uint16_t* v, void* out, int n_splits, nexus_stream_t stream);
 
+    // ---- device-resident KV cache (the attention half of q35_full_layer) ----
+    //
+    // One decode token of a full-attention layer over a KV cache kept in HBM, replacing
+    // the attention part of VulkanBackend::q35_full_layer (src/gpu/vulkan_backend.h:
+    // 5272-5483): the per-(owner, layer) mirror is found or grown, tokens the host changed
+    // or the mirror never had are copied from the host cache (which stays the source of
+    // truth), then the prep kernel (head norms, RoPE, store of row `pos`) and the gated
+    // split-KV decode run over the mirror.  The projections before and the output
+    // projection after stay with the caller: qg / k_raw / v_raw and attn_out are device
+    // f32 buffers the engine's own matvecs produce and consume.
+    struct KvLayerDesc {                                 // vulkan_backend.h:491-515, attention fields
+        const void* owner = nullptr;
+        int layer = 0;
+        uint32_t n_heads = 0, n_kv = 0, hd = 0, rot = 0, pos = 0;
+        float norm_eps = 1e-6f, scale = 0.f;             // scale 0: 1/sqrt(hd)
+        bool has_gate = true;                            // qg holds [q | gate] per head
+        bool rope_interleaved = false;
+        const float* q_norm = nullptr;                   // host [hd] or nullptr (no q head norm)
+        const float* k_norm = nullptr;
+        bool q_zc = false, k_zc = false;                 // (1 + w) norms
+        const float* rope_tab = nullptr;                 // host [rot]: cos then sin for `pos`
+        const uint16_t* const* k_host = nullptr;         // [n_kv] -> host f16 [tokens][hd]
+        const uint16_t* const* v_host = nullptr;
+        uint32_t host_tokens = 0;                        // tokens on the host (>= pos)
+        uint32_t host_synced = 0;                        // host rows [0, host_synced) unchanged since the last sync
+    };
+    // Synchronous like the reference's call: returns once kv_out_host ([2][n_kv][hd] f32,
+    // K then V of token `pos` as stored, for KVCache::store) is written; attn_out is
+    // ready on `stream` (nullptr: the backend's stream).  *mirror_valid_out = pos + 1,
+    // the value for KVCache::set_mirror_valid.  Declines (false, nothing touched) on an
+    // unsupported shape, null pointers, host_tokens < pos, or when the mirror would
+    // exceed the budget (then it also remembers the refused size, as the reference does).
+    bool q35_attention(const KvLayerDesc& d, const float* qg, const float* k_raw, const float* v_raw,
+                       float* attn_out, float* kv_out_host, uint32_t* mirror_valid_out,
+                       nexus_stream_t stream = nullptr);
+    // Free the mirrors of `owner`: one layer, or all of them when layer < 0
+    // (vulkan_backend.h:5207-5217).
+    void q35_kv_drop(const void* owner, int layer);
+    // Mirror budget in MiB: -1 auto (free HBM now plus the mirrors' own bytes, less a
+    // margin of max(768 MiB, 1/5 of HBM) and 64 MiB of scratch), 0 off, N at most N MiB.
+    // The NEXUS_GPU_KV environment variable ("off", "auto", or MiB) sets the start value.
+    void set_gpu_kv_mb(int mb);
+    int gpu_kv_mb();
+    size_t kv_mirror_used() const { return kv_mirror_used_; }
+    size_t kv_mirror_cap_bytes();
+    // Row store of the mirror: truncating (default, bit-identical to the host cache that
+    // stores the returned K/V with KVCache::store) or round-to-nearest-even (the shader's
+    // packHalf2x16).
+    void set_mirror_store_rne(bool rne) { mirror_rne_ = rne; }
+    // Introspection for tests and logs.
+    bool kv_mirror_info(const void* owner, int layer, size_t* cap, size_t* valid);
+    bool kv_mirror_read(const void* owner, int layer, int kv_head, int pos0, int n, uint16_t* k_out,
+                        uint16_t* v_out);
+
     // Counters for tests and logs.
     long long calls_run() const { return calls_run_; }
     long long calls_declined() const { return calls_declined_; }
@@ -109,7 +165,21 @@ private:
     bool run_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
                     const uint16_t* v, void* out, int n_splits, bool decode, void* stream);
 
+    struct KvMirror {                                    // vulkan_backend.h:823
+        DevBuf k, v;
+        size_t cap = 0, valid = 0, bytes = 0, refused_need = 0;
+        uint32_t n_kv = 0, hd = 0;
+    };
+    bool alloc_exact(DevBuf& b, size_t bytes);
+    void free_buf(DevBuf& b);
+    void drop_locked(const void* owner, int layer);
+
     std::mutex mu_;
+    std::map<std::pair<const void*, int>, KvMirror> mirrors_;
+    size_t kv_mirror_used_ = 0;
+    int gpu_kv_mb_ = -2;                                 // -2: not read from the environment yet
+    bool mirror_rne_ = false;
+    DevBuf prep_q_, prep_gate_, prep_kv_, prep_par_;
     bool ready_ = false;
     int device_ = -1;
     void* stream_ = nullptr;                 // hipStream_t

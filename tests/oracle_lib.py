@@ -161,6 +161,7 @@ def decode_prep(qg, kraw, vraw, qnw, knw, tab, *, n_heads, n_kv, hd, rot, flags,
                 kc=None, vc=None, rne=False):
     """One token of the decode prep (oracle_decode_prep).  Returns (q_out, gate_out, kc, vc,
     kv_out); kc/vc are [n_kv][cap][hd] f16 bit arrays (updated copies when given)."""
+    assert 0 <= pos < cap, "the K/V row `pos` must lie inside the cap rows"
     qg, kraw, vraw = _c(qg, np.float32).reshape(-1), _c(kraw, np.float32).reshape(-1), _c(vraw, np.float32).reshape(-1)
     qnw = _c(qnw if qnw is not None else np.zeros(hd), np.float32)
     knw = _c(knw if knw is not None else np.zeros(hd), np.float32)

@@ -370,7 +370,7 @@ def test_prep_rope_vs_reference_rope_apply(layout):
     tab = np.concatenate([np.cos(theta.astype(np.float64)), np.sin(theta.astype(np.float64))]).astype(np.float32)
     flags = O.PREP_NO_GATE | O.PREP_NO_QNORM | O.PREP_NO_KNORM | (O.PREP_INTERLEAVED if layout == 0 else 0)
     q_out, *_ = O.decode_prep(x, x, x, None, None, tab, n_heads=1, n_kv=1, hd=hd, rot=hd, flags=flags,
-                              eps=1e-6, pos=pos, cap=1)
+                              eps=1e-6, pos=0, cap=1)           # the angle is in the table; pos is the store row
     np.testing.assert_allclose(q_out[0], O.ref_rope(x[0], pos, hd, base, layout), rtol=0, atol=6e-5)
 
 
