@@ -56,7 +56,8 @@ enum nexus_status {
     NEXUS_E_UNSUPPORTED   = -1,   /* shape the kernels do not cover (declined, like nx_decline) */
     NEXUS_E_INVALID       = -2,   /* null pointer or inconsistent argument */
     NEXUS_E_WORKSPACE     = -3,   /* workspace missing or too small for the requested split */
-    NEXUS_E_LAUNCH        = -4    /* the HIP runtime refused the launch */
+    NEXUS_E_LAUNCH        = -4,   /* the HIP runtime refused the launch or a copy */
+    NEXUS_E_IO            = -5    /* a file could not be opened, read or written (nexus_hip_kv.h) */
 };
 
 /* One attention call.  Mirrors the push constants of attn_flash.comp:18-31

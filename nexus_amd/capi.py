@@ -22,8 +22,9 @@ NEXUS_E_UNSUPPORTED = -1
 NEXUS_E_INVALID = -2
 NEXUS_E_WORKSPACE = -3
 NEXUS_E_LAUNCH = -4
+NEXUS_E_IO = -5
 
-# Every symbol include/nexus_hip_attn.h declares (checked by tests/test_capi.py).
+# Every symbol include/*.h declares (checked by tests/test_capi.py).
 EXPORTED_SYMBOLS = (
     "nexus_hip_attn_prefill",
     "nexus_hip_attn_prefill_ws_bytes",
@@ -33,6 +34,14 @@ EXPORTED_SYMBOLS = (
     "nexus_hip_attn_prefill_gated",
     "nexus_hip_attn_decode_gated",
     "nexus_hip_attn_decode_prep",
+    "nexus_hip_kv_layer_bytes",
+    "nexus_hip_kv_cache_bytes",
+    "nexus_hip_kv_layer_save",
+    "nexus_hip_kv_layer_load",
+    "nexus_hip_kv_cache_save",
+    "nexus_hip_kv_cache_load",
+    "nexus_hip_kv_cache_save_file",
+    "nexus_hip_kv_cache_load_file",
     "nexus_hip_attn_last_error",
     "nexus_hip_attn_version",
 )
@@ -92,6 +101,18 @@ class PrepDesc(ctypes.Structure):
     ]
 
 
+class KvLayerView(ctypes.Structure):
+    """struct nexus_kv_layer_view (include/nexus_hip_kv.h)."""
+
+    _fields_ = [
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("n_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("row_stride", ctypes.c_int64),
+    ]
+
+
 class NexusAttnError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"nexus_hip_attn status {code}: {msg}")
@@ -129,6 +150,21 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.nexus_hip_attn_decode_gated.restype = ctypes.c_int
     lib.nexus_hip_attn_decode_prep.argtypes = [ctypes.POINTER(PrepDesc)] + [vp] * 12
     lib.nexus_hip_attn_decode_prep.restype = ctypes.c_int
+    kvp = ctypes.POINTER(KvLayerView)
+    ip = ctypes.POINTER(ctypes.c_int)
+    lib.nexus_hip_kv_layer_bytes.argtypes = [kvp, ctypes.c_int]
+    lib.nexus_hip_kv_layer_bytes.restype = sz
+    lib.nexus_hip_kv_cache_bytes.argtypes = [kvp, ctypes.c_int, ctypes.c_int]
+    lib.nexus_hip_kv_cache_bytes.restype = sz
+    lib.nexus_hip_kv_layer_save.argtypes = [ctypes.c_int, kvp, ctypes.c_int, vp, sz, vp]
+    lib.nexus_hip_kv_layer_load.argtypes = [vp, sz, kvp, ctypes.c_int, ip, ip, vp]
+    lib.nexus_hip_kv_cache_save.argtypes = [kvp, ctypes.c_int, ctypes.c_int, vp, sz, vp]
+    lib.nexus_hip_kv_cache_load.argtypes = [vp, sz, kvp, ctypes.c_int, ip, vp]
+    lib.nexus_hip_kv_cache_save_file.argtypes = [ctypes.c_char_p, kvp, ctypes.c_int, ctypes.c_int, vp]
+    lib.nexus_hip_kv_cache_load_file.argtypes = [ctypes.c_char_p, kvp, ctypes.c_int, ip, vp]
+    for name in ("nexus_hip_kv_layer_save", "nexus_hip_kv_layer_load", "nexus_hip_kv_cache_save",
+                 "nexus_hip_kv_cache_load", "nexus_hip_kv_cache_save_file", "nexus_hip_kv_cache_load_file"):
+        getattr(lib, name).restype = ctypes.c_int
     lib.nexus_hip_attn_last_error.argtypes = []
     lib.nexus_hip_attn_last_error.restype = ctypes.c_char_p
     lib.nexus_hip_attn_version.argtypes = []

@@ -15,12 +15,13 @@
 #include <cstdio>
 
 #include "attn_kernels.h"
+#include "capi_status.h"
 
 namespace {
-
 thread_local char g_last_error[512] = "";
+}  // namespace
 
-int fail(int code, const char* fmt, ...)
+int nxa::capi_fail(int code, const char* fmt, ...)
 {
     va_list ap;
     va_start(ap, fmt);
@@ -29,11 +30,16 @@ int fail(int code, const char* fmt, ...)
     return code;
 }
 
-int ok()
+int nxa::capi_ok()
 {
     g_last_error[0] = '\0';
     return NEXUS_OK;
 }
+
+namespace {
+
+using nxa::capi_fail;
+int ok() { return nxa::capi_ok(); }
 
 constexpr int kMaxDevices = 64;
 using nxa::kMaxSplits;
@@ -65,28 +71,28 @@ bool supported_head_dim(int hd) { return hd == 64 || hd == 128 || hd == 192 || h
 // or > 256, Hq % Hkv != 0, non-positive sizes (vulkan_backend.h:4270-4273).
 int check_desc(const nexus_attn_desc* d)
 {
-    if (!d) return fail(NEXUS_E_INVALID, "desc is NULL");
+    if (!d) return capi_fail(NEXUS_E_INVALID, "desc is NULL");
     if (d->n_q_heads <= 0 || d->n_kv_heads <= 0 || d->n_q_heads % d->n_kv_heads != 0)
-        return fail(NEXUS_E_UNSUPPORTED, "n_q_heads=%d must be a positive multiple of n_kv_heads=%d",
+        return capi_fail(NEXUS_E_UNSUPPORTED, "n_q_heads=%d must be a positive multiple of n_kv_heads=%d",
                     d->n_q_heads, d->n_kv_heads);
     if (!supported_head_dim(d->head_dim))
-        return fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in {64,128,192,256}", d->head_dim);
+        return capi_fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in {64,128,192,256}", d->head_dim);
     if (d->n_query <= 0 || d->n_ctx <= 0 || d->q_base_pos < 0)
-        return fail(NEXUS_E_INVALID, "n_query=%d n_ctx=%d q_base_pos=%d", d->n_query, d->n_ctx, d->q_base_pos);
+        return capi_fail(NEXUS_E_INVALID, "n_query=%d n_ctx=%d q_base_pos=%d", d->n_query, d->n_ctx, d->q_base_pos);
     if ((long long)d->q_base_pos + d->n_query > INT_MAX - 4096 || d->n_ctx > INT_MAX - 4096)
-        return fail(NEXUS_E_UNSUPPORTED, "positions exceed the 31-bit range");
+        return capi_fail(NEXUS_E_UNSUPPORTED, "positions exceed the 31-bit range");
     if ((long long)d->n_ctx * d->head_dim * 2 >= (1LL << 31))
-        return fail(NEXUS_E_UNSUPPORTED, "n_ctx * head_dim exceeds the 2 GiB per-kv-head buffer range");
+        return capi_fail(NEXUS_E_UNSUPPORTED, "n_ctx * head_dim exceeds the 2 GiB per-kv-head buffer range");
     if ((long long)d->n_query * d->n_q_heads * d->head_dim * 4 >= (1LL << 31))
-        return fail(NEXUS_E_UNSUPPORTED, "n_query * n_q_heads * head_dim exceeds the 2 GiB query buffer range");
+        return capi_fail(NEXUS_E_UNSUPPORTED, "n_query * n_q_heads * head_dim exceeds the 2 GiB query buffer range");
     if (d->kv_row_stride < d->n_ctx)
-        return fail(NEXUS_E_INVALID, "kv_row_stride=%lld < n_ctx=%d", (long long)d->kv_row_stride, d->n_ctx);
-    if (d->sliding_window < 0) return fail(NEXUS_E_INVALID, "sliding_window=%d", d->sliding_window);
-    if (!(d->scale >= 0.f) || !std::isfinite(d->scale)) return fail(NEXUS_E_INVALID, "scale=%g", (double)d->scale);
-    if (!(d->softcap >= 0.f) || !std::isfinite(d->softcap)) return fail(NEXUS_E_INVALID, "softcap=%g", (double)d->softcap);
+        return capi_fail(NEXUS_E_INVALID, "kv_row_stride=%lld < n_ctx=%d", (long long)d->kv_row_stride, d->n_ctx);
+    if (d->sliding_window < 0) return capi_fail(NEXUS_E_INVALID, "sliding_window=%d", d->sliding_window);
+    if (!(d->scale >= 0.f) || !std::isfinite(d->scale)) return capi_fail(NEXUS_E_INVALID, "scale=%g", (double)d->scale);
+    if (!(d->softcap >= 0.f) || !std::isfinite(d->softcap)) return capi_fail(NEXUS_E_INVALID, "softcap=%g", (double)d->softcap);
     if ((d->q_dtype != NEXUS_DT_F32 && d->q_dtype != NEXUS_DT_F16) ||
         (d->o_dtype != NEXUS_DT_F32 && d->o_dtype != NEXUS_DT_F16))
-        return fail(NEXUS_E_UNSUPPORTED, "q_dtype=%d o_dtype=%d", d->q_dtype, d->o_dtype);
+        return capi_fail(NEXUS_E_UNSUPPORTED, "q_dtype=%d o_dtype=%d", d->q_dtype, d->o_dtype);
     return NEXUS_OK;
 }
 
@@ -231,7 +237,7 @@ int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, const flo
     c.n_rows = d->n_query * d->n_q_heads;
     c.n_splits = n_splits;
     const hipError_t e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
-    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e));
     return NEXUS_OK;
 }
 
@@ -271,7 +277,7 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.row_tiles = decode_row_tiles(d);
     hipError_t e = nxa::launch_decode(a, d->head_dim, d->q_dtype == NEXUS_DT_F32, d->o_dtype == NEXUS_DT_F32,
                                       is_ext(d), decode_rowgroups(d), stream);
-    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "decode launch: %s", hipGetErrorString(e));
     if (n_splits > 1) {
         const int rc = launch_combine_for(d, ws, out, gate, n_splits, stream);
         if (rc != NEXUS_OK) return rc;
@@ -303,11 +309,11 @@ int nexus_hip_attn_decode_gated(const nexus_attn_desc* desc, const void* q, cons
 {
     const int rc = check_desc(desc);
     if (rc != NEXUS_OK) return rc;
-    if (!q || !k || !v || !out) return fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
-    if (!partial_ws) return fail(NEXUS_E_WORKSPACE, "partial_ws is NULL");
-    if (gate && ((uintptr_t)gate & 15u)) return fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
+    if (!q || !k || !v || !out) return capi_fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
+    if (!partial_ws) return capi_fail(NEXUS_E_WORKSPACE, "partial_ws is NULL");
+    if (gate && ((uintptr_t)gate & 15u)) return capi_fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
     if (n_splits <= 0) n_splits = default_decode_splits(desc);
-    if (n_splits > kMaxSplits) return fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
+    if (n_splits > kMaxSplits) return capi_fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
     return run_decode(desc, q, k, v, out, gate, partial_ws, n_splits, (hipStream_t)stream);
 }
 
@@ -329,25 +335,25 @@ int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, c
                                const float* rope_tab, float* q_out, float* gate_out, uint16_t* k_cache,
                                uint16_t* v_cache, float* kv_out, nexus_stream_t stream)
 {
-    if (!d) return fail(NEXUS_E_INVALID, "desc is NULL");
+    if (!d) return capi_fail(NEXUS_E_INVALID, "desc is NULL");
     if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_heads > 65536 || d->n_kv_heads > 65536)
-        return fail(NEXUS_E_INVALID, "n_heads=%d n_kv_heads=%d", d->n_heads, d->n_kv_heads);
+        return capi_fail(NEXUS_E_INVALID, "n_heads=%d n_kv_heads=%d", d->n_heads, d->n_kv_heads);
     if (d->head_dim <= 0 || d->head_dim > nxa::kPrepMaxHeadDim)
-        return fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in [1, %d]", d->head_dim, nxa::kPrepMaxHeadDim);
+        return capi_fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in [1, %d]", d->head_dim, nxa::kPrepMaxHeadDim);
     if (d->rot_dims < 0 || d->rot_dims > d->head_dim || (d->rot_dims & 1))
-        return fail(NEXUS_E_INVALID, "rot_dims=%d must be even and in [0, head_dim=%d]", d->rot_dims, d->head_dim);
+        return capi_fail(NEXUS_E_INVALID, "rot_dims=%d must be even and in [0, head_dim=%d]", d->rot_dims, d->head_dim);
     if (d->cap <= 0 || d->pos < 0 || d->pos >= d->cap)
-        return fail(NEXUS_E_INVALID, "pos=%d outside the cache rows [0, cap=%lld)", d->pos, (long long)d->cap);
-    if (d->flags & ~127) return fail(NEXUS_E_INVALID, "unknown flag bits 0x%x", d->flags & ~127);
-    if (!(d->eps >= 0.f) || !std::isfinite(d->eps)) return fail(NEXUS_E_INVALID, "eps=%g", (double)d->eps);
-    if (d->reserved != 0) return fail(NEXUS_E_INVALID, "reserved=%d must be 0", d->reserved);
+        return capi_fail(NEXUS_E_INVALID, "pos=%d outside the cache rows [0, cap=%lld)", d->pos, (long long)d->cap);
+    if (d->flags & ~127) return capi_fail(NEXUS_E_INVALID, "unknown flag bits 0x%x", d->flags & ~127);
+    if (!(d->eps >= 0.f) || !std::isfinite(d->eps)) return capi_fail(NEXUS_E_INVALID, "eps=%g", (double)d->eps);
+    if (d->reserved != 0) return capi_fail(NEXUS_E_INVALID, "reserved=%d must be 0", d->reserved);
     const bool gated = (d->flags & NEXUS_PREP_NO_GATE) == 0;
     if (!qg || !k_raw || !v_raw || !q_out || !k_cache || !v_cache || !kv_out)
-        return fail(NEXUS_E_INVALID, "null qg/k_raw/v_raw/q_out/k_cache/v_cache/kv_out pointer");
-    if (gated && !gate_out) return fail(NEXUS_E_INVALID, "gate_out is NULL for a gated layer");
-    if (!(d->flags & NEXUS_PREP_NO_Q_NORM) && !q_norm_w) return fail(NEXUS_E_INVALID, "q_norm_w is NULL");
-    if (!(d->flags & NEXUS_PREP_NO_K_NORM) && !k_norm_w) return fail(NEXUS_E_INVALID, "k_norm_w is NULL");
-    if (d->rot_dims > 0 && !rope_tab) return fail(NEXUS_E_INVALID, "rope_tab is NULL");
+        return capi_fail(NEXUS_E_INVALID, "null qg/k_raw/v_raw/q_out/k_cache/v_cache/kv_out pointer");
+    if (gated && !gate_out) return capi_fail(NEXUS_E_INVALID, "gate_out is NULL for a gated layer");
+    if (!(d->flags & NEXUS_PREP_NO_Q_NORM) && !q_norm_w) return capi_fail(NEXUS_E_INVALID, "q_norm_w is NULL");
+    if (!(d->flags & NEXUS_PREP_NO_K_NORM) && !k_norm_w) return capi_fail(NEXUS_E_INVALID, "k_norm_w is NULL");
+    if (d->rot_dims > 0 && !rope_tab) return capi_fail(NEXUS_E_INVALID, "rope_tab is NULL");
 
     nxa::PrepArgs a{};
     a.qg = qg;
@@ -370,7 +376,7 @@ int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, c
     a.flags = d->flags;
     a.eps = d->eps;
     const hipError_t e = nxa::launch_decode_prep(a, (hipStream_t)stream);
-    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "decode prep launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "decode prep launch: %s", hipGetErrorString(e));
     return ok();
 }
 
@@ -389,8 +395,8 @@ int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, con
 {
     const int rc = check_desc(desc);
     if (rc != NEXUS_OK) return rc;
-    if (!q || !k || !v || !out) return fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
-    if (gate && ((uintptr_t)gate & 15u)) return fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
+    if (!q || !k || !v || !out) return capi_fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
+    if (gate && ((uintptr_t)gate & 15u)) return capi_fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
 
     // A handful of queries (speculative verify, tiny prompts): the split-KV kernel fills
@@ -427,12 +433,12 @@ int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, con
     a.n_qblocks = (int)((desc->n_query + rows - 1) / rows);
     a.n_splits = splits;
     const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
-    if (items > INT_MAX) return fail(NEXUS_E_UNSUPPORTED, "grid too large");
+    if (items > INT_MAX) return capi_fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
     const bool q32 = desc->q_dtype == NEXUS_DT_F32, o32 = desc->o_dtype == NEXUS_DT_F32;
     hipError_t e = plan.wide ? nxa::launch_prefill_wide(a, desc->head_dim, plan.ks, q32, o32, s)
                              : nxa::launch_prefill(a, desc->head_dim, q32, o32, is_ext(desc), s);
-    if (e != hipSuccess) return fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
     if (splits > 1) {
         const int rc2 = launch_combine_for(desc, (float*)workspace, out, gate, splits, s);
         if (rc2 != NEXUS_OK) return rc2;

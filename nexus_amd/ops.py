@@ -9,6 +9,9 @@ live on a HIP device: there is no CPU path here, a declined call raises NexusAtt
 """
 from __future__ import annotations
 
+import ctypes
+
+import numpy as np
 import torch
 
 from . import capi
@@ -153,3 +156,91 @@ def decode_prep(qg: torch.Tensor, k_raw: torch.Tensor, v_raw: torch.Tensor, k_ca
                          ptr(rope_tab), q_out.data_ptr(), ptr(gate_out if gated else None), k_cache.data_ptr(),
                          v_cache.data_ptr(), kv_out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
     return q_out, (gate_out if gated else None), kv_out
+
+
+# ------------------------------------------------------------------ KV session files
+
+def _kv_views(layers):
+    """layers: per model layer, (k, v) device tensors [n_kv, row_stride, hd] of f16 bits, or
+    None for a layer without KV."""
+    arr = (capi.KvLayerView * len(layers))()
+    dev = None
+    for i, lv in enumerate(layers):
+        if lv is None:
+            arr[i] = capi.KvLayerView(None, None, 0, 0, 0)
+            continue
+        k, v = lv
+        for name, t in (("k", k), ("v", v)):
+            if not t.is_cuda or not t.is_contiguous() or t.dim() != 3:
+                raise RuntimeError(f"layer {i} {name}: a contiguous [n_kv, row_stride, hd] device tensor is needed")
+            _kv_view(t)
+        if k.shape != v.shape:
+            raise ValueError(f"layer {i}: k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+        dev = k.device
+        arr[i] = capi.KvLayerView(k.data_ptr(), v.data_ptr(), k.shape[0], k.shape[2], k.shape[1])
+    return arr, dev
+
+
+def _kv_stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream if dev is not None else None
+
+
+def kv_cache_bytes(layers, n_tokens: int) -> int:
+    views, _ = _kv_views(layers)
+    return int(capi.load().nexus_hip_kv_cache_bytes(views, len(layers), n_tokens))
+
+
+def kv_cache_save(layers, n_tokens: int):
+    """NXKVCACH image of rows [0, n_tokens) (KVCache::save_to_buffer) as a uint8 numpy array."""
+    views, dev = _kv_views(layers)
+    lib = capi.load()
+    buf = np.empty(lib.nexus_hip_kv_cache_bytes(views, len(layers), n_tokens), np.uint8)
+    capi._check(lib.nexus_hip_kv_cache_save(views, len(layers), n_tokens, buf.ctypes.data, buf.nbytes,
+                                            _kv_stream(dev)))
+    return buf
+
+
+def kv_cache_load(data, layers) -> int:
+    """Apply an NXKVCACH image (KVCache::load_from_buffer); returns its token count."""
+    buf = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data, np.uint8)
+    views, dev = _kv_views(layers)
+    n = ctypes.c_int(0)
+    capi._check(capi.load().nexus_hip_kv_cache_load(buf.ctypes.data, buf.nbytes, views, len(layers), n,
+                                                    _kv_stream(dev)))
+    return n.value
+
+
+def kv_layer_save(layer: int, k: torch.Tensor, v: torch.Tensor, n_tokens: int):
+    """NXKVLYR1 record of one layer (KVCache::save_layer_to_buffer) as a uint8 numpy array."""
+    views, dev = _kv_views([(k, v)])
+    lib = capi.load()
+    size = lib.nexus_hip_kv_layer_bytes(views, n_tokens)
+    buf = np.empty(max(1, size), np.uint8)
+    capi._check(lib.nexus_hip_kv_layer_save(layer, views, n_tokens, buf.ctypes.data, size, _kv_stream(dev)))
+    return buf[:size]
+
+
+def kv_layer_load(data, layers) -> tuple[int, int]:
+    """Apply an NXKVLYR1 record (KVCache::load_layer_from_buffer); returns (layer, n_tokens)."""
+    buf = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data, np.uint8)
+    views, dev = _kv_views(layers)
+    layer, n = ctypes.c_int(0), ctypes.c_int(0)
+    capi._check(capi.load().nexus_hip_kv_layer_load(buf.ctypes.data, buf.nbytes, views, len(layers), layer, n,
+                                                    _kv_stream(dev)))
+    return layer.value, n.value
+
+
+def kv_cache_save_file(path, layers, n_tokens: int) -> None:
+    """KVCache::save(path) from device memory, streamed through pinned staging."""
+    views, dev = _kv_views(layers)
+    capi._check(capi.load().nexus_hip_kv_cache_save_file(str(path).encode(), views, len(layers), n_tokens,
+                                                         _kv_stream(dev)))
+
+
+def kv_cache_load_file(path, layers) -> int:
+    """KVCache::load(path) straight into device memory; returns the token count."""
+    views, dev = _kv_views(layers)
+    n = ctypes.c_int(0)
+    capi._check(capi.load().nexus_hip_kv_cache_load_file(str(path).encode(), views, len(layers), n,
+                                                         _kv_stream(dev)))
+    return n.value

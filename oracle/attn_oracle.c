@@ -22,6 +22,9 @@
  *                         nx_apply_projection_norm_inplace does (transformer.h:580-618);
  *                         RoPE as rope_apply (model/attention.h:491-608) with the angle table
  *                         supplied; K/V store with kvcache.h:903-911 or :256-274 conversion
+ *   oracle_kv_*           NXKVCACH / NXKVLYR1 images (model/kvcache.h:352-551): the
+ *                         save_to_buffer / save_layer_to_buffer byte layout, the legacy
+ *                         layout load_from_buffer still accepts, and both loaders
  *   oracle_naive_f64      independent float64 brute force (checker only)
  *
  * How each function is pinned (tests/test_oracle.py):
@@ -36,6 +39,8 @@
  *                  forms (one key, zero query, one-hot key, window of one);
  *   split/combine  split-vs-unsplit identity (LSE associativity) for many chunkings;
  *   gate_mul       against scipy's expit inside (-80, 80) and the clamp values outside;
+ *   kv session     byte-for-byte against the reference's own KVCache writers and loaders
+ *                  (oracle/_ref) and against fixtures they wrote (tests/golden);
  *   decode_prep    norm against the reference's own cpu::rms_norm (oracle/_ref), the (1+w)
  *                  form against it with 1+w weights; RoPE against the reference's own
  *                  rope_apply with the same angles, identity/composition/norm-preserving
@@ -396,6 +401,123 @@ void oracle_decode_prep(int n_heads, int n_kv, int hd, int rot, int flags, float
         }
     }
     free(row);
+}
+
+/* ------------------------------------------------------------ KV session formats */
+
+/* Header geometry: the largest head count / head dim over the layers (KVCache::init_per_layer,
+ * kvcache.h:88-109). */
+static void kv_header_geometry(int n_layers, const int* nh, const int* hd, int32_t* mh, int32_t* md)
+{
+    *mh = 0;
+    *md = 0;
+    for (int l = 0; l < n_layers; ++l) {
+        if (nh[l] > *mh) *mh = nh[l];
+        if (hd[l] > *md) *md = hd[l];
+    }
+}
+
+static uint8_t* kv_put_header(uint8_t* p, const char* magic, int32_t a, int32_t b, int32_t c, int32_t d)
+{
+    const int32_t hdr[4] = {a, b, c, d};
+    memcpy(p, magic, 8);
+    memcpy(p + 8, hdr, sizeof(hdr));
+    return p + 24;
+}
+
+/* K then V of every head of one layer, rows [0, n_tok); K == NULL writes zeros. */
+static uint8_t* kv_put_layer(uint8_t* p, int nh, int hd, const uint16_t* K, const uint16_t* V, long stride, int n_tok)
+{
+    const size_t blk = (size_t)n_tok * (size_t)hd * 2;
+    for (int h = 0; h < nh; ++h) {
+        const size_t off = (size_t)h * (size_t)stride * (size_t)hd;
+        if (K) memcpy(p, K + off, blk); else memset(p, 0, blk);
+        p += blk;
+        if (V) memcpy(p, V + off, blk); else memset(p, 0, blk);
+        p += blk;
+    }
+    return p;
+}
+
+long oracle_kv_cache_save(int n_layers, const int* nh, const int* hd, const uint16_t* const* K,
+                          const uint16_t* const* V, long stride, int n_tok, uint8_t* out, long cap, int legacy)
+{
+    int32_t mh, md;
+    kv_header_geometry(n_layers, nh, hd, &mh, &md);
+    size_t total = 24;
+    for (int l = 0; l < n_layers; ++l) {
+        const int h = legacy ? mh : nh[l], d = legacy ? md : hd[l];
+        total += (size_t)h * (size_t)n_tok * (size_t)d * 4;
+    }
+    if ((long)total > cap) return (long)total;
+    uint8_t* p = kv_put_header(out, "NXKVCACH", n_layers, mh, md, n_tok);
+    for (int l = 0; l < n_layers; ++l) {
+        if (legacy && nh[l] == 0) p = kv_put_layer(p, mh, md, NULL, NULL, 0, n_tok);
+        else p = kv_put_layer(p, nh[l], hd[l], K[l], V[l], stride, n_tok);
+    }
+    return (long)total;
+}
+
+long oracle_kv_layer_save(int layer, int nh, int hd, const uint16_t* K, const uint16_t* V, long stride, int n_tok,
+                          uint8_t* out, long cap)
+{
+    if (nh == 0) return 0;
+    const size_t total = 24 + (size_t)nh * (size_t)n_tok * (size_t)hd * 4;
+    if ((long)total > cap) return (long)total;
+    kv_put_layer(kv_put_header(out, "NXKVLYR1", layer, nh, hd, n_tok), nh, hd, K, V, stride, n_tok);
+    return (long)total;
+}
+
+static const uint8_t* kv_get_layer(const uint8_t* p, int nh, int hd, uint16_t* K, uint16_t* V, long stride, int n_tok)
+{
+    const size_t blk = (size_t)n_tok * (size_t)hd * 2;
+    for (int h = 0; h < nh; ++h) {
+        const size_t off = (size_t)h * (size_t)stride * (size_t)hd;
+        memcpy(K + off, p, blk);
+        p += blk;
+        memcpy(V + off, p, blk);
+        p += blk;
+    }
+    return p;
+}
+
+int oracle_kv_cache_load(int n_layers, const int* nh, const int* hd, const uint8_t* data, long size,
+                         uint16_t* const* K, uint16_t* const* V, long stride)
+{
+    int32_t mh, md, hdr[4];
+    if (size < 24 || memcmp(data, "NXKVCACH", 8) != 0) return -1;
+    memcpy(hdr, data + 8, sizeof(hdr));
+    kv_header_geometry(n_layers, nh, hd, &mh, &md);
+    if (hdr[0] != n_layers || hdr[1] != mh || hdr[2] != md || hdr[3] < 0 || hdr[3] > stride) return -1;
+    const int n_tok = hdr[3];
+    size_t cur = 24, old = 24;
+    for (int l = 0; l < n_layers; ++l) {
+        cur += (size_t)nh[l] * (size_t)n_tok * (size_t)hd[l] * 4;
+        old += (size_t)mh * (size_t)n_tok * (size_t)md * 4;
+    }
+    const int legacy = old != cur && (size_t)size == old;
+    if (!legacy && (size_t)size < cur) return -1;
+    const uint8_t* p = data + 24;
+    for (int l = 0; l < n_layers; ++l) {
+        if (legacy && nh[l] == 0) { p += (size_t)mh * (size_t)n_tok * (size_t)md * 4; continue; }
+        if (p + (size_t)nh[l] * (size_t)n_tok * (size_t)hd[l] * 4 > data + size) return -1;
+        p = kv_get_layer(p, nh[l], hd[l], K[l], V[l], stride, n_tok);
+    }
+    return n_tok;
+}
+
+int oracle_kv_layer_load(int n_layers, const int* nh, const int* hd, const uint8_t* data, long size,
+                         uint16_t* const* K, uint16_t* const* V, long stride, int* layer_out)
+{
+    int32_t hdr[4];
+    if (size < 24 || memcmp(data, "NXKVLYR1", 8) != 0) return -1;
+    memcpy(hdr, data + 8, sizeof(hdr));
+    const int l = hdr[0];
+    if (l < 0 || l >= n_layers || hdr[1] != nh[l] || hdr[2] != hd[l] || hdr[3] < 0 || hdr[3] > stride) return -1;
+    if (24 + (size_t)nh[l] * (size_t)hdr[3] * (size_t)hd[l] * 4 > (size_t)size) return -1;
+    kv_get_layer(data + 24, nh[l], hd[l], K[l], V[l], stride, hdr[3]);
+    *layer_out = l;
+    return hdr[3];
 }
 
 /* ------------------------------------------------------------ float64 brute force */

@@ -83,6 +83,19 @@ void oracle_naive_f64(const float* Q, const uint16_t* K, const uint16_t* V, doub
                       int n_ctx, long kv_stride, int n_query, int q_base_pos,
                       int sliding_window, double scale, double softcap);
 
+/* KV session formats (model/kvcache.h:352-551).  Layer l: nh[l] heads of dim hd[l], rows of
+ * head h at K[l] + h * stride * hd[l].  Savers return the image size (written when <= cap);
+ * legacy != 0 writes every layer at the header geometry (zero blocks for nh[l] == 0).
+ * Loaders return the token count, or -1 where the reference refuses the image. */
+long oracle_kv_cache_save(int n_layers, const int* nh, const int* hd, const uint16_t* const* K,
+                          const uint16_t* const* V, long stride, int n_tok, uint8_t* out, long cap, int legacy);
+long oracle_kv_layer_save(int layer, int nh, int hd, const uint16_t* K, const uint16_t* V, long stride, int n_tok,
+                          uint8_t* out, long cap);
+int oracle_kv_cache_load(int n_layers, const int* nh, const int* hd, const uint8_t* data, long size,
+                         uint16_t* const* K, uint16_t* const* V, long stride);
+int oracle_kv_layer_load(int n_layers, const int* nh, const int* hd, const uint8_t* data, long size,
+                         uint16_t* const* K, uint16_t* const* V, long stride, int* layer_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,6 +7,9 @@
 //   nexus::model::KVCache::{init, store, write_raw, read_raw, set_n_tokens, pack_k, pack_v}
 //                                                          model/kvcache.h:69-78,148-178,214-241,655-672
 //   nexus::model::KVCache::f32_to_f16_rne                  model/kvcache.h:256-274
+//   nexus::model::KVCache::{init_per_layer, save, save_to_buffer, save_layer_to_buffer,
+//                           load_from_buffer, load_layer_from_buffer}
+//                                                          model/kvcache.h:88-109,352-551
 //   nexus::quant::f16_to_f32                               gguf/quant.h:128-161
 //   nexus::cpu::rms_norm                                   cpu/matmul.h:1860-1880
 //   nexus::model::rope_apply                               model/attention.h:491-608
@@ -92,6 +95,107 @@ void ref_rope_apply(float* x, int pos, int head_dim, float freq_base, int layout
     cfg.freq_base = freq_base;
     cfg.layout = layout;
     nexus::model::rope_apply(x, pos, head_dim, cfg);
+}
+
+// ---- KV session formats through the reference's own KVCache (kvcache.h:352-551).
+// Geometry: layer l has nh[l] kv heads of dim hd[l] (per_layer != 0: init_per_layer, else
+// init with nh[0]/hd[0] for every layer).  Rows of layer l, head h live at
+// K[l] + h * stride * hd[l] (and V[l]); a layer with K[l] == NULL stays empty.
+
+namespace {
+void ref_kv_build(KVCache& kv, int n_layers, const int* nh, const int* hd, int per_layer)
+{
+    if (per_layer) kv.init_per_layer(std::vector<int>(nh, nh + n_layers), std::vector<int>(hd, hd + n_layers));
+    else kv.init(n_layers, nh[0], hd[0]);
+}
+
+int ref_kv_fill(KVCache& kv, int n_layers, const int* nh, const int* hd, const uint16_t* const* K,
+                const uint16_t* const* V, long stride, int n_tok)
+{
+    for (int l = 0; l < n_layers; ++l) {
+        if (!K[l] || n_tok == 0) continue;
+        for (int h = 0; h < nh[l]; ++h) {
+            const size_t off = (size_t)h * (size_t)stride * (size_t)hd[l];
+            if (!kv.write_raw(l, h, 0, n_tok, K[l] + off, V[l] + off)) return -1;
+        }
+    }
+    kv.set_n_tokens(n_tok);
+    return 0;
+}
+
+long ref_kv_out(const std::vector<uint8_t>& buf, uint8_t* out, long cap)
+{
+    if ((long)buf.size() <= cap && !buf.empty()) std::memcpy(out, buf.data(), buf.size());
+    return (long)buf.size();
+}
+
+int ref_kv_read(KVCache& kv, int n_layers, const int* nh, uint16_t* const* K, uint16_t* const* V, long stride,
+                const int* hd, int n_tok)
+{
+    for (int l = 0; l < n_layers; ++l) {
+        if (!K[l] || n_tok == 0) continue;
+        for (int h = 0; h < nh[l]; ++h) {
+            const size_t off = (size_t)h * (size_t)stride * (size_t)hd[l];
+            if (!kv.read_raw(l, h, 0, n_tok, K[l] + off, V[l] + off)) return -1;
+        }
+    }
+    return 0;
+}
+}  // namespace
+
+// save_to_buffer (NXKVCACH): returns the image size (copied to out when it fits).
+long ref_kv_save_cache(int n_layers, const int* nh, const int* hd, int per_layer, const uint16_t* const* K,
+                       const uint16_t* const* V, long stride, int n_tok, uint8_t* out, long cap)
+{
+    KVCache kv;
+    ref_kv_build(kv, n_layers, nh, hd, per_layer);
+    if (ref_kv_fill(kv, n_layers, nh, hd, K, V, stride, n_tok) != 0) return -1;
+    return ref_kv_out(kv.save_to_buffer(), out, cap);
+}
+
+// save(path) (NXKVCACH file): 0 on success.
+int ref_kv_save_file(const char* path, int n_layers, const int* nh, const int* hd, int per_layer,
+                     const uint16_t* const* K, const uint16_t* const* V, long stride, int n_tok)
+{
+    KVCache kv;
+    ref_kv_build(kv, n_layers, nh, hd, per_layer);
+    if (ref_kv_fill(kv, n_layers, nh, hd, K, V, stride, n_tok) != 0) return -1;
+    return kv.save(path) ? 0 : -1;
+}
+
+// save_layer_to_buffer (NXKVLYR1) of `layer`.
+long ref_kv_save_layer(int n_layers, const int* nh, const int* hd, int per_layer, const uint16_t* const* K,
+                       const uint16_t* const* V, long stride, int n_tok, int layer, uint8_t* out, long cap)
+{
+    KVCache kv;
+    ref_kv_build(kv, n_layers, nh, hd, per_layer);
+    if (ref_kv_fill(kv, n_layers, nh, hd, K, V, stride, n_tok) != 0) return -1;
+    return ref_kv_out(kv.save_layer_to_buffer(layer), out, cap);
+}
+
+// load_from_buffer (NXKVCACH) into a fresh cache, rows read back with read_raw: returns the
+// token count, or -1 when the reference refuses the image.
+int ref_kv_load_cache(int n_layers, const int* nh, const int* hd, int per_layer, const uint8_t* data, long size,
+                      uint16_t* const* K, uint16_t* const* V, long stride)
+{
+    KVCache kv;
+    ref_kv_build(kv, n_layers, nh, hd, per_layer);
+    if (!kv.load_from_buffer(data, (size_t)size)) return -1;
+    const int n_tok = kv.n_tokens();
+    if (n_tok > stride || ref_kv_read(kv, n_layers, nh, K, V, stride, hd, n_tok) != 0) return -1;
+    return n_tok;
+}
+
+// load_layer_from_buffer (NXKVLYR1) into a fresh cache: returns the token count afterwards.
+int ref_kv_load_layer(int n_layers, const int* nh, const int* hd, int per_layer, const uint8_t* data, long size,
+                      uint16_t* const* K, uint16_t* const* V, long stride)
+{
+    KVCache kv;
+    ref_kv_build(kv, n_layers, nh, hd, per_layer);
+    if (!kv.load_layer_from_buffer(data, (size_t)size)) return -1;
+    const int n_tok = kv.n_tokens();
+    if (n_tok > stride || ref_kv_read(kv, n_layers, nh, K, V, stride, hd, n_tok) != 0) return -1;
+    return n_tok;
 }
 
 }  // extern "C"

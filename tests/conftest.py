@@ -20,6 +20,13 @@ def golden():
 
 
 @pytest.fixture(scope="session")
+def golden_kv():
+    import numpy as np
+
+    return np.load(ROOT / "tests" / "golden" / "golden_kv.npz")
+
+
+@pytest.fixture(scope="session")
 def hip():
     """The native library on a real GPU (gpu tests only).  No fallback: fails loudly."""
     import torch

@@ -18,7 +18,10 @@ _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i, _l, _f, _d = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double
+_vp = ctypes.c_void_p
+_vpp = ctypes.POINTER(ctypes.c_void_p)
 
 _oracle = None
 _ref = None
@@ -49,6 +52,14 @@ def oracle() -> ctypes.CDLL:
         lib.oracle_gate_mul.argtypes = [_f32p, _f32p, ctypes.c_size_t]
         lib.oracle_decode_prep.argtypes = [_i, _i, _i, _i, _i, _f, _i, _l, _f32p, _f32p, _f32p, _f32p, _f32p,
                                            _f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _i]
+        lib.oracle_kv_cache_save.argtypes = [_i, _i32p, _i32p, _vpp, _vpp, _l, _i, _u8p, _l, _i]
+        lib.oracle_kv_cache_save.restype = _l
+        lib.oracle_kv_layer_save.argtypes = [_i, _i, _i, _vp, _vp, _l, _i, _u8p, _l]
+        lib.oracle_kv_layer_save.restype = _l
+        lib.oracle_kv_cache_load.argtypes = [_i, _i32p, _i32p, _u8p, _l, _vpp, _vpp, _l]
+        lib.oracle_kv_cache_load.restype = _i
+        lib.oracle_kv_layer_load.argtypes = [_i, _i32p, _i32p, _u8p, _l, _vpp, _vpp, _l, ctypes.POINTER(_i)]
+        lib.oracle_kv_layer_load.restype = _i
         _oracle = lib
     return _oracle
 
@@ -75,6 +86,16 @@ def ref() -> ctypes.CDLL:
         lib.ref_f16_to_f32.restype = _f
         lib.ref_rms_norm.argtypes = [_f32p, _f32p, _f32p, _l, _f]
         lib.ref_rope_apply.argtypes = [_f32p, _i, _i, _f, _i]
+        lib.ref_kv_save_cache.argtypes = [_i, _i32p, _i32p, _i, _vpp, _vpp, _l, _i, _u8p, _l]
+        lib.ref_kv_save_cache.restype = _l
+        lib.ref_kv_save_file.argtypes = [ctypes.c_char_p, _i, _i32p, _i32p, _i, _vpp, _vpp, _l, _i]
+        lib.ref_kv_save_file.restype = _i
+        lib.ref_kv_save_layer.argtypes = [_i, _i32p, _i32p, _i, _vpp, _vpp, _l, _i, _i, _u8p, _l]
+        lib.ref_kv_save_layer.restype = _l
+        lib.ref_kv_load_cache.argtypes = [_i, _i32p, _i32p, _i, _u8p, _l, _vpp, _vpp, _l]
+        lib.ref_kv_load_cache.restype = _i
+        lib.ref_kv_load_layer.argtypes = [_i, _i32p, _i32p, _i, _u8p, _l, _vpp, _vpp, _l]
+        lib.ref_kv_load_layer.restype = _i
         _ref = lib
     return _ref
 
@@ -209,3 +230,128 @@ def rel_l2(a, b) -> float:
     b = np.asarray(b, np.float64)
     den = np.sqrt(np.sum(b * b))
     return float(np.sqrt(np.sum((a - b) ** 2)) / max(den, 1e-30))
+
+
+# ------------------------------------------------------------------ KV session formats
+
+class KvCache:
+    """A host-side multi-layer cache for the session-format checks: layer l holds K and V
+    as uint16 [nh_l, stride, hd_l] (None for a layer without KV, or an empty slot)."""
+
+    def __init__(self, geom, stride, k=None, v=None):
+        self.geom = [(int(h), int(d)) for h, d in geom]
+        self.stride = int(stride)
+        n = len(self.geom)
+        self.k = list(k) if k is not None else [None] * n
+        self.v = list(v) if v is not None else [None] * n
+
+    @classmethod
+    def random(cls, geom, stride, seed, empty=()):
+        rng = np.random.default_rng(seed)
+        c = cls(geom, stride)
+        for l, (h, d) in enumerate(c.geom):
+            if h and l not in empty:
+                c.k[l] = rng.integers(0, 1 << 16, (h, stride, d), dtype=np.uint16)
+                c.v[l] = rng.integers(0, 1 << 16, (h, stride, d), dtype=np.uint16)
+        return c
+
+    @classmethod
+    def zeros(cls, geom, stride):
+        c = cls(geom, stride)
+        for l, (h, d) in enumerate(c.geom):
+            if h:
+                c.k[l] = np.zeros((h, stride, d), np.uint16)
+                c.v[l] = np.zeros((h, stride, d), np.uint16)
+        return c
+
+    def nh(self):
+        return np.array([g[0] for g in self.geom], np.int32)
+
+    def hd(self):
+        return np.array([g[1] for g in self.geom], np.int32)
+
+    def ptrs(self, which):
+        arr = self.k if which == "k" else self.v
+        out = (ctypes.c_void_p * len(arr))()
+        for i, a in enumerate(arr):
+            out[i] = None if a is None else a.ctypes.data
+        return out
+
+
+def kv_cache_save(c: KvCache, n_tok, legacy=False) -> bytes:
+    lib = oracle()
+    args = (len(c.geom), c.nh(), c.hd(), c.ptrs("k"), c.ptrs("v"), c.stride, n_tok)
+    size = lib.oracle_kv_cache_save(*args, np.zeros(1, np.uint8), 0, int(legacy))
+    out = np.zeros(size, np.uint8)
+    assert lib.oracle_kv_cache_save(*args, out, size, int(legacy)) == size
+    return out.tobytes()
+
+
+def kv_layer_save(c: KvCache, layer, n_tok) -> bytes:
+    lib = oracle()
+    h, d = c.geom[layer]
+    k = None if c.k[layer] is None else c.k[layer].ctypes.data
+    v = None if c.v[layer] is None else c.v[layer].ctypes.data
+    size = lib.oracle_kv_layer_save(layer, h, d, k, v, c.stride, n_tok, np.zeros(1, np.uint8), 0)
+    out = np.zeros(max(size, 1), np.uint8)
+    assert lib.oracle_kv_layer_save(layer, h, d, k, v, c.stride, n_tok, out, size) == size
+    return out[:size].tobytes()
+
+
+def kv_cache_load(data: bytes, geom, stride):
+    """Returns (n_tok, KvCache) or (-1, None)."""
+    c = KvCache.zeros(geom, stride)
+    buf = np.frombuffer(data, np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    n = oracle().oracle_kv_cache_load(len(c.geom), c.nh(), c.hd(), buf, len(data), c.ptrs("k"), c.ptrs("v"), stride)
+    return (n, c) if n >= 0 else (-1, None)
+
+
+def kv_layer_load(data: bytes, geom, stride):
+    """Returns (n_tok, layer, KvCache) or (-1, -1, None)."""
+    c = KvCache.zeros(geom, stride)
+    buf = np.frombuffer(data, np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    layer = ctypes.c_int(-1)
+    n = oracle().oracle_kv_layer_load(len(c.geom), c.nh(), c.hd(), buf, len(data), c.ptrs("k"), c.ptrs("v"),
+                                      stride, ctypes.byref(layer))
+    return (n, layer.value, c) if n >= 0 else (-1, -1, None)
+
+
+def ref_kv_save_cache(c: KvCache, n_tok, per_layer) -> bytes:
+    lib = ref()
+    args = (len(c.geom), c.nh(), c.hd(), int(per_layer), c.ptrs("k"), c.ptrs("v"), c.stride, n_tok)
+    size = lib.ref_kv_save_cache(*args, np.zeros(1, np.uint8), 0)
+    assert size >= 0
+    out = np.zeros(size, np.uint8)
+    assert lib.ref_kv_save_cache(*args, out, size) == size
+    return out.tobytes()
+
+
+def ref_kv_save_file(path, c: KvCache, n_tok, per_layer):
+    assert ref().ref_kv_save_file(str(path).encode(), len(c.geom), c.nh(), c.hd(), int(per_layer), c.ptrs("k"),
+                                  c.ptrs("v"), c.stride, n_tok) == 0
+
+
+def ref_kv_save_layer(c: KvCache, layer, n_tok, per_layer) -> bytes:
+    lib = ref()
+    args = (len(c.geom), c.nh(), c.hd(), int(per_layer), c.ptrs("k"), c.ptrs("v"), c.stride, n_tok, layer)
+    size = lib.ref_kv_save_layer(*args, np.zeros(1, np.uint8), 0)
+    assert size >= 0
+    out = np.zeros(max(size, 1), np.uint8)
+    assert lib.ref_kv_save_layer(*args, out, size) == size
+    return out[:size].tobytes()
+
+
+def ref_kv_load_cache(data: bytes, geom, stride, per_layer):
+    c = KvCache.zeros(geom, stride)
+    buf = np.frombuffer(data, np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    n = ref().ref_kv_load_cache(len(c.geom), c.nh(), c.hd(), int(per_layer), buf, len(data), c.ptrs("k"),
+                                c.ptrs("v"), stride)
+    return (n, c) if n >= 0 else (-1, None)
+
+
+def ref_kv_load_layer(data: bytes, geom, stride, per_layer):
+    c = KvCache.zeros(geom, stride)
+    buf = np.frombuffer(data, np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    n = ref().ref_kv_load_layer(len(c.geom), c.nh(), c.hd(), int(per_layer), buf, len(data), c.ptrs("k"),
+                                c.ptrs("v"), stride)
+    return (n, c) if n >= 0 else (-1, None)

@@ -11,11 +11,12 @@ import pytest
 from nexus_amd import capi
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "nexus_hip_attn.h"
+HEADERS = sorted(HEADER.parent.glob("*.h"))
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(nexus_hip_attn_[a-z_0-9]+)\s*\(", text, re.M)))
+    text = "\n".join(h.read_text() for h in HEADERS)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(nexus_hip_[a-z_0-9]+)\s*\(", text, re.M)))
 
 
 def test_header_declares_what_the_binding_knows():
@@ -29,7 +30,8 @@ def test_library_exports_every_declared_symbol():
     assert "gfx950" in capi.version()
 
 
-@pytest.mark.parametrize("cls,cname", [(capi.AttnDesc, "nexus_attn_desc"), (capi.PrepDesc, "nexus_attn_prep_desc")])
+@pytest.mark.parametrize("cls,cname", [(capi.AttnDesc, "nexus_attn_desc"), (capi.PrepDesc, "nexus_attn_prep_desc"),
+                                       (capi.KvLayerView, "nexus_kv_layer_view")])
 def test_desc_layout_matches_header(tmp_path, cls, cname):
     """The ctypes mirrors of the descriptors have the C compiler's size and offsets."""
     import shutil
@@ -40,7 +42,8 @@ def test_desc_layout_matches_header(tmp_path, cls, cname):
         pytest.skip("no C compiler on this host")
     fields = [f[0] for f in cls._fields_]
     src = tmp_path / "layout.c"
-    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "nexus_hip_attn.h"\nint main(void){'
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "nexus_hip_attn.h"\n#include "nexus_hip_kv.h"\n'
+                   'int main(void){'
                    f'printf("%zu", sizeof({cname}));'
                    + "".join(f'printf(" %zu", offsetof({cname}, {f}));' for f in fields)
                    + "return 0;}\n")
@@ -171,3 +174,61 @@ def test_prep_null_pointers_declined():
     assert capi.decode_prep_raw(d, p, p, p, p, p, 0, o, o, o, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # table
     assert capi.decode_prep_raw(d, p, p, p, p, p, p, o, o, 0, o, o, 0, check=False) == capi.NEXUS_E_INVALID   # k cache
     assert np.all(out == 7.0)
+
+
+# ------------------------------------------------------------------ KV session entry points
+
+def _kv_views(geom, stride, ptr=None):
+    arr = (capi.KvLayerView * len(geom))()
+    for i, (h, d) in enumerate(geom):
+        arr[i] = capi.KvLayerView(ptr if h else None, ptr if h else None, h, d, stride)
+    return arr
+
+
+def test_kv_sizes_match_the_reference_images(golden_kv):
+    """nexus_hip_kv_*_bytes agree with the images the reference's KVCache wrote."""
+    lib = capi.load()
+    for name, geom, stride, n_tok in (("uniform", [(2, 64)] * 3, 8, 5),
+                                      ("per_layer", [(2, 64), (0, 0), (4, 128), (1, 256), (0, 0)], 7, 6)):
+        views = _kv_views(geom, stride)
+        assert lib.nexus_hip_kv_cache_bytes(views, len(geom), n_tok) == golden_kv[f"{name}_image"].size
+        for l in range(len(geom)):
+            assert lib.nexus_hip_kv_layer_bytes(ctypes.byref(views[l]), n_tok) == golden_kv[f"{name}_layer{l}"].size
+
+
+def test_kv_declines_before_any_copy(golden_kv):
+    """Bad images and impossible requests are refused during validation: no device needed,
+    nothing written (the reference's loader can stop part-way; this one checks first)."""
+    lib = capi.load()
+    geom, stride, n_tok = [(2, 64), (0, 0), (4, 128), (1, 256), (0, 0)], 7, 6
+    sentinel = np.full(4096, 7, np.uint16)
+    views = _kv_views(geom, stride, sentinel.ctypes.data)
+    img = golden_kv["per_layer_image"]
+    n = ctypes.c_int(-9)
+    bad_images = [img[:-1], img[:20], np.concatenate([np.frombuffer(b"NXKVCACX", np.uint8), img[8:]])]
+    for data in bad_images:
+        data = np.ascontiguousarray(data)
+        assert lib.nexus_hip_kv_cache_load(data.ctypes.data, data.size, views, len(geom), ctypes.byref(n), None) == \
+            capi.NEXUS_E_INVALID
+    other = _kv_views([(2, 64), (0, 0), (4, 128), (1, 128), (0, 0)], stride, sentinel.ctypes.data)  # other model
+    assert lib.nexus_hip_kv_cache_load(img.ctypes.data, img.size, other, len(geom), ctypes.byref(n), None) == \
+        capi.NEXUS_E_INVALID
+    assert b"model mismatch" in capi.load().nexus_hip_attn_last_error()
+    short = _kv_views(geom, n_tok - 1, sentinel.ctypes.data)                 # capacity below the image's tokens
+    assert lib.nexus_hip_kv_cache_load(img.ctypes.data, img.size, short, len(geom), ctypes.byref(n), None) == \
+        capi.NEXUS_E_INVALID
+    rec = golden_kv["per_layer_layer2"]
+    wrong = _kv_views([(2, 64), (0, 0), (4, 64), (1, 256), (0, 0)], stride, sentinel.ctypes.data)
+    lo = ctypes.c_int(-9)
+    for data, v in ((rec[:-1], views), (rec, wrong)):
+        data = np.ascontiguousarray(data)
+        assert lib.nexus_hip_kv_layer_load(data.ctypes.data, data.size, v, len(geom), ctypes.byref(lo),
+                                           ctypes.byref(n), None) == capi.NEXUS_E_INVALID
+    out = np.full(64, 5, np.uint8)
+    assert lib.nexus_hip_kv_cache_save(views, len(geom), n_tok, out.ctypes.data, out.size, None) == \
+        capi.NEXUS_E_INVALID                                              # buffer too small
+    assert lib.nexus_hip_kv_cache_save(views, len(geom), stride + 1, out.ctypes.data, 1 << 30, None) == \
+        capi.NEXUS_E_INVALID                                              # more tokens than rows
+    assert lib.nexus_hip_kv_cache_load_file(b"/nonexistent/kv.bin", views, len(geom), ctypes.byref(n), None) == \
+        capi.NEXUS_E_IO
+    assert np.all(sentinel == 7) and np.all(out == 5) and n.value == -9 and lo.value == -9

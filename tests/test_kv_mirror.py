@@ -54,20 +54,28 @@ def trunc16(x):
     return out
 
 
+def rne16(x):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(x.size, np.uint16)
+    O.oracle().nx_f32_to_f16_rne_n(x, out, x.size)
+    return out
+
+
 class HostLayer:
     """One layer of the host KVCache: f16 [n_kv][cap][hd] plus its mirror_valid
     (src/model/kvcache.h:148-178, 224-241, 276-285)."""
 
-    def __init__(self, n_kv, hd, cap):
+    def __init__(self, n_kv, hd, cap, rne=False):
         self.k = np.zeros((n_kv, cap, hd), np.uint16)
         self.v = np.zeros((n_kv, cap, hd), np.uint16)
         self.n_tokens = 0
         self.mirror_valid = 0
+        self.conv = rne16 if rne else trunc16           # KVCache::store truncates (kvcache.h:903-911)
 
-    def store(self, pos, kv_out):                      # KVCache::store with the truncating conversion
+    def store(self, pos, kv_out):
         n_kv, _, hd = self.k.shape
-        self.k[:, pos] = trunc16(kv_out[0]).reshape(n_kv, hd)
-        self.v[:, pos] = trunc16(kv_out[1]).reshape(n_kv, hd)
+        self.k[:, pos] = self.conv(kv_out[0]).reshape(n_kv, hd)
+        self.v[:, pos] = self.conv(kv_out[1]).reshape(n_kv, hd)
         self.mirror_valid = min(self.mirror_valid, pos)
         self.n_tokens = max(self.n_tokens, pos + 1)
 
@@ -106,7 +114,8 @@ def fill_prompt(layer, rng, n):
 
 
 def step(layer, rng, pos, owner, layer_id=0, expect_ok=True):
-    """One decode token through the backend; returns the device output (checked when it ran)."""
+    """One decode token through the backend; returns (device output, returned K/V), both
+    checked, when it ran."""
     import torch
 
     lib = shim()
@@ -149,7 +158,7 @@ def step(layer, rng, pos, owner, layer_id=0, expect_ok=True):
     ma, rl = O.max_abs(got, ref), O.rel_l2(got, ref)
     print(f"[mirror] pos={pos} max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
     assert ma < 2e-3 and rl < 1e-3, (ma, rl)
-    return got
+    return got, kv_out
 
 
 def mirror_info(owner, layer_id=0):
@@ -279,22 +288,23 @@ def test_budget_refusal_and_shape_change(hip):
 
 
 @pytest.mark.gpu
-def test_mirror_rne_store_differs_only_in_rounding(hip):
-    """With the shader's round-to-nearest-even store the mirror row of each new token is
-    the RNE conversion of the returned K/V (the host keeps its truncated copy)."""
+def test_mirror_rne_store(hip):
+    """With the shader's round-to-nearest-even store each new mirror row is the RNE
+    conversion of the returned K/V: a host that stores with RNE too sees its own rows in the
+    mirror, and they differ from the truncating store by at most one unit in the last place."""
     rng = np.random.default_rng(11)
     lib = shim()
     owner = 0x8001
     L = Layer(rng, host_cap=64)
+    L.host = HostLayer(L.n_kv, L.hd, 64, rne=True)
+    fill_prompt(L, rng, 5)
     try:
         lib.shim_set_mirror_store_rne(1)
-        step(L, rng, 0, owner)
-        kv_host_trunc = L.host.k[:, 0].copy()
-        k = np.zeros((1, L.hd), np.uint16)
-        v = np.zeros((1, L.hd), np.uint16)
-        assert lib.shim_kv_mirror_read(owner, 0, 0, 0, 1, k.reshape(-1), v.reshape(-1)) == 1
-        # RNE and truncation agree or differ by one unit in the last place
-        diff = np.abs(k[0].astype(np.int32) - kv_host_trunc[0].astype(np.int32))
+        for pos in range(5, 8):
+            _, kv_out = step(L, rng, pos, owner)
+        assert_mirror_equals_host(L, owner, 8)
+        rne = rne16(kv_out).astype(np.int32)
+        diff = np.abs(rne - trunc16(kv_out).astype(np.int32))
         assert diff.max() <= 1 and diff.sum() > 0
     finally:
         lib.shim_set_mirror_store_rne(0)

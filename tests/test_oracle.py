@@ -425,3 +425,113 @@ def test_prep_layout_gate_and_store():
             keep = np.ones(cap, bool)
             keep[pos] = False
             np.testing.assert_array_equal(cache[:, keep], c0[:, keep])
+
+
+# ------------------------------------------------------------------ KV session formats
+
+KV_UNIFORM = ([(2, 64)] * 3, 8, 5, False)                                   # geom, stride, n_tok, per_layer
+KV_PER_LAYER = ([(2, 64), (0, 0), (4, 128), (1, 256), (0, 0)], 7, 6, True)   # layers without KV, mixed dims
+KV_CASES = {"uniform": KV_UNIFORM, "per_layer": KV_PER_LAYER}
+
+
+@needs_ref
+@pytest.mark.parametrize("name", list(KV_CASES))
+@pytest.mark.parametrize("n_tok_delta", [0, -2])
+def test_kv_cache_image_matches_reference(name, n_tok_delta, tmp_path):
+    """NXKVCACH bytes: the restatement == KVCache::save_to_buffer == KVCache::save(path);
+    a layer whose slots were never written is saved as zeros."""
+    geom, stride, n_tok, per_layer = KV_CASES[name]
+    n_tok += n_tok_delta
+    c = O.KvCache.random(geom, stride, seed=1, empty=(2,) if name == "per_layer" else ())
+    mine = O.kv_cache_save(c, n_tok)
+    ref = O.ref_kv_save_cache(c, n_tok, per_layer)
+    assert mine == ref
+    O.ref_kv_save_file(tmp_path / "kv.bin", c, n_tok, per_layer)
+    assert (tmp_path / "kv.bin").read_bytes() == ref
+    hdr = np.frombuffer(ref[8:24], np.int32)
+    assert ref[:8] == b"NXKVCACH" and list(hdr) == [len(geom), max(g[0] for g in geom), max(g[1] for g in geom), n_tok]
+
+
+@needs_ref
+@pytest.mark.parametrize("name", list(KV_CASES))
+def test_kv_layer_record_matches_reference(name):
+    geom, stride, n_tok, per_layer = KV_CASES[name]
+    c = O.KvCache.random(geom, stride, seed=2)
+    for l in range(len(geom)):
+        mine = O.kv_layer_save(c, l, n_tok)
+        assert mine == O.ref_kv_save_layer(c, l, n_tok, per_layer), l
+        assert (mine == b"") == (geom[l][0] == 0)
+
+
+def _same_rows(a, b, n_tok):
+    for l, (h, _) in enumerate(a.geom):
+        if h:
+            np.testing.assert_array_equal(a.k[l][:, :n_tok], b.k[l][:, :n_tok])
+            np.testing.assert_array_equal(a.v[l][:, :n_tok], b.v[l][:, :n_tok])
+
+
+@needs_ref
+@pytest.mark.parametrize("name", list(KV_CASES))
+def test_kv_loaders_agree_with_reference(name):
+    """Each loader reads the other's image back to the same rows; a record restores its layer."""
+    geom, stride, n_tok, per_layer = KV_CASES[name]
+    c = O.KvCache.random(geom, stride, seed=3)
+    n, back = O.kv_cache_load(O.ref_kv_save_cache(c, n_tok, per_layer), geom, stride)
+    assert n == n_tok
+    _same_rows(back, c, n_tok)
+    n, back = O.ref_kv_load_cache(O.kv_cache_save(c, n_tok), geom, stride, per_layer)
+    assert n == n_tok
+    _same_rows(back, c, n_tok)
+    l = 2 if name == "per_layer" else 1
+    rec = O.kv_layer_save(c, l, n_tok)
+    n, layer, mine = O.kv_layer_load(rec, geom, stride)
+    nr, theirs = O.ref_kv_load_layer(rec, geom, stride, per_layer)
+    assert (n, layer) == (n_tok, l) and nr == n_tok
+    for x in (mine, theirs):
+        np.testing.assert_array_equal(x.k[l][:, :n_tok], c.k[l][:, :n_tok])
+        np.testing.assert_array_equal(x.v[l][:, :n_tok], c.v[l][:, :n_tok])
+
+
+@needs_ref
+def test_kv_legacy_layout_read_like_the_reference():
+    """The legacy image (every layer at the header geometry, zero blocks for layers without KV)
+    is what the reference's loader still accepts: it reads the restatement's legacy image to
+    the same rows as the restatement's own loader."""
+    geom, stride, n_tok, _ = KV_PER_LAYER
+    geom = [(4, 128), (0, 0), (4, 128), (0, 0)]          # KV layers at the header geometry
+    c = O.KvCache.random(geom, stride, seed=4)
+    legacy = O.kv_cache_save(c, n_tok, legacy=True)
+    assert len(legacy) > len(O.kv_cache_save(c, n_tok))
+    n, theirs = O.ref_kv_load_cache(legacy, geom, stride, True)
+    assert n == n_tok
+    _same_rows(theirs, c, n_tok)
+    n, mine = O.kv_cache_load(legacy, geom, stride)
+    assert n == n_tok
+    _same_rows(mine, c, n_tok)
+
+
+@needs_ref
+def test_kv_refusals_agree_with_reference():
+    geom, stride, n_tok, per_layer = KV_PER_LAYER
+    c = O.KvCache.random(geom, stride, seed=5)
+    img = O.kv_cache_save(c, n_tok)
+    bad = [img[:-1], b"NXKVCACX" + img[8:], img[:20]]
+    other = [(2, 64), (0, 0), (4, 128), (1, 128), (0, 0)]  # a different model
+    for data, g in [(x, geom) for x in bad] + [(img, other)]:
+        assert O.kv_cache_load(data, g, stride)[0] == -1
+        assert O.ref_kv_load_cache(data, g, stride, per_layer)[0] == -1
+    rec = O.kv_layer_save(c, 3, n_tok)
+    for data in (rec[:-1], b"NXKVLYR2" + rec[8:]):
+        assert O.kv_layer_load(data, geom, stride)[0] == -1
+        assert O.ref_kv_load_layer(data, geom, stride, per_layer)[0] == -1
+
+
+def test_kv_images_vs_golden(golden_kv):
+    """The restatement reproduces the images the reference wrote (tests/golden/golden_kv.npz)."""
+    g = golden_kv
+    for name, (geom, stride, n_tok, _) in KV_CASES.items():
+        c = O.KvCache(geom, stride, [g.get(f"{name}_k{l}") for l in range(len(geom))],
+                      [g.get(f"{name}_v{l}") for l in range(len(geom))])
+        assert O.kv_cache_save(c, n_tok) == g[f"{name}_image"].tobytes()
+        for l in range(len(geom)):
+            assert O.kv_layer_save(c, l, n_tok) == g[f"{name}_layer{l}"].tobytes()
