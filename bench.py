@@ -137,6 +137,89 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False) -> dict:
     return res
 
 
+def measure_decode_layer(steps: int, warmup: int) -> dict:
+    """The attention half of a gated full-attention decode layer over a device KV cache
+    (q35_full_layer's prep + part + comb): decode prep (q/k head norms, partial RoPE, f16
+    store of the new row) then gated split-KV decode, one token at 32768 cached tokens,
+    16 q / 2 kv heads, head_dim 256, RoPE over 64 dims.  The prep alone and the whole step
+    are timed with HIP events on the stream they run on."""
+    import torch
+
+    from nexus_amd import capi, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    nh, nkv, hd, rot, pos = 16, 2, 256, 64, 32768
+    cap = ((pos + 1) * 5 // 4 + 255) // 256 * 256
+    kv_bytes = 2 * nkv * cap * hd * 2
+    n_sets = max(2, min(64, -(-2 * MALL_BYTES // kv_bytes)))
+    caches = [(torch.randn(nkv, cap, hd, generator=g, device=dev).half(),
+               torch.randn(nkv, cap, hd, generator=g, device=dev).half()) for _ in range(n_sets)]
+    qg = torch.randn(nh, 2 * hd, generator=g, device=dev)
+    kraw = torch.randn(nkv, hd, generator=g, device=dev)
+    vraw = torch.randn(nkv, hd, generator=g, device=dev)
+    qnw = 0.1 * torch.randn(hd, generator=g, device=dev)
+    knw = 0.1 * torch.randn(hd, generator=g, device=dev)
+    ang = pos / torch.pow(torch.tensor(1e7, device=dev), torch.arange(rot // 2, device=dev) * 2.0 / rot)
+    tab = torch.cat([torch.cos(ang), torch.sin(ang)]).float()
+    q_out = torch.empty(nh, hd, device=dev)
+    gate = torch.empty(nh, hd, device=dev)
+    kvo = torch.empty(2, nkv, hd, device=dev)
+    out = torch.empty(1, nh, hd, device=dev)
+    desc = capi.make_desc(n_q_heads=nh, n_kv_heads=nkv, head_dim=hd, n_query=1, q_base_pos=pos, n_ctx=pos + 1,
+                          kv_row_stride=cap)
+    splits = capi.decode_default_splits(desc)
+    ws = torch.empty(capi.decode_ws_bytes(desc, splits) // 4, device=dev)
+    pdesc = capi.PrepDesc(nh, nkv, hd, rot, pos, capi.PREP_Q_NORM_ADD_ONE | capi.PREP_K_NORM_ADD_ONE
+                          | capi.PREP_TRUNC_STORE, cap, 1e-6, 0)
+    # a warm call through the checked wrapper, then raw C-ABI calls captured in a HIP graph:
+    # the step is a few microseconds of GPU work, so host-side launch cost must stay out
+    ops.decode_prep(qg, kraw, vraw, caches[0][0], caches[0][1], pos=pos, rope_tab=tab, q_norm_w=qnw, k_norm_w=knw,
+                    q_norm_add_one=True, k_norm_add_one=True, trunc_store=True, q_out=q_out, gate_out=gate, kv_out=kvo)
+
+    def prep(i, stream):
+        k, v = caches[i % n_sets]
+        capi.decode_prep_raw(pdesc, qg.data_ptr(), kraw.data_ptr(), vraw.data_ptr(), qnw.data_ptr(), knw.data_ptr(),
+                             tab.data_ptr(), q_out.data_ptr(), gate.data_ptr(), k.data_ptr(), v.data_ptr(),
+                             kvo.data_ptr(), stream)
+
+    def step(i, stream):
+        prep(i, stream)
+        k, v = caches[i % n_sets]
+        capi.decode_raw(desc, q_out.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr(), splits,
+                        stream, gate=gate.data_ptr())
+
+    def timed(fn):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for i in range(warmup):
+            fn(i, stream)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            cap_stream = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(steps):
+                fn(i, cap_stream)
+        gr.replay()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        gr.replay()
+        s1.record()
+        s1.synchronize()
+        return s0.elapsed_time(s1) / steps
+
+    ms_prep, ms_step = timed(prep), timed(step)
+    kv_read = 2.0 * nkv * (pos + 1) * hd * 2
+    res = {"config": "decode_layer", "desc": "gated decode layer attention over a device KV cache: prep + "
+           "split-KV decode + gated combine, 1 token at 32768 cached tokens, 16q/2kv, hd256, rot 64",
+           "ms": ms_step, "prep_ms": ms_prep, "splits": splits, "kv_sets": n_sets, "launch": "graph",
+           "gbs": kv_read / (ms_step * 1e-3) / 1e9, "frac_hbm": kv_read / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    log(f"[bench] decode_layer: {ms_step * 1e3:.1f} us/step (prep {ms_prep * 1e3:.1f} us)  "
+        f"{res['gbs']:.0f} GB/s of K/V ({100 * res['frac_hbm']:.1f}% HBM)")
+    return res
+
+
 def copy_calibration(steps: int, warmup: int, nbytes: int = 256 << 20) -> None:
     """A plain elementwise copy of known size (torch.mul by 1 over float32: each launch reads
     and writes nbytes): the reference point that scales the rocprofv3 FETCH_SIZE /
@@ -232,7 +315,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy"], default=None,
+    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy", "decode_layer"], default=None,
                     help="measure one config only (for profiling runs); 'copy' runs a plain "
                          "device copy of 256 MiB that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -254,6 +337,9 @@ def main() -> int:
     if args.only == "copy":
         copy_calibration(args.steps, args.warmup)
         return 0
+    if args.only == "decode_layer":
+        measure_decode_layer(args.steps, args.warmup)
+        return 0
     if args.only:
         measure(args.only, args.steps, args.warmup)
         return 0
@@ -264,6 +350,7 @@ def main() -> int:
         steps = max(5, args.steps // 5) if name == "cfg3" else args.steps
         extra[name] = measure(name, steps, args.warmup)
     extra["cfg1_graph"] = measure("cfg1", args.steps, args.warmup, graph=True)
+    extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -149,7 +149,11 @@ int default_decode_splits(const nexus_attn_desc* d)
     key_range(d, &kb, &ke);
     const long long kv_len = ke - kb;
     const long long base = (long long)d->n_kv_heads * decode_rowgroups(d);
-    const long long target = (long long)decode_wg_per_cu(d) * device_cus();
+    // About one workgroup per CU above head dim 128, two up to it: a split of a 256-dim
+    // head is only one or two K/V steps per wave at 2 per CU, and its fixed cost (Q staging,
+    // the cross-wave merge, the partial) then outweighs the extra streams -- measured on
+    // MI355X at 32k keys: 16q/2kv hd256 fastest at 128 splits (1 query) / 64 (4 drafts).
+    const long long target = (long long)(d->head_dim > 128 ? 1 : decode_wg_per_cu(d)) * device_cus();
     long long s = target / base;
     if (s < 1) s = 1;
     const long long by_len = (kv_len + 127) / 128;           // keep >= 128 keys (one step per wave)
