@@ -140,6 +140,7 @@ int decode_rowgroups(const nexus_attn_desc* d)
 // Workgroups resident at once per CU for the decode kernel (its register budget).
 int decode_wg_per_cu(const nexus_attn_desc* d)
 {
+    if (nxa::decode_waves(d->head_dim, decode_row_tiles(d)) == 8) return 1;   // 8 waves: one per CU
     return d->head_dim * decode_row_tiles(d) <= 256 ? 2 : 1;     // decode_waves_per_simd
 }
 

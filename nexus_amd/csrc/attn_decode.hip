@@ -48,6 +48,7 @@ constexpr int decode_depth(int hd, int rt) { return hd * rt <= 128 ? 2 : (hd * r
 
 template <int HD, int RT>
 struct DecodeLayout {
+    static constexpr int NW = decode_waves(HD, RT);               // waves per workgroup
     static constexpr int KEYS = kDecodeKeys;                  // 32 keys per wave step
     static constexpr int KS = HD / 32;                        // 32-dim k-steps of S^T
     static constexpr int DT = HD / 16;                        // 16-dim tiles of O^T
@@ -57,7 +58,7 @@ struct DecodeLayout {
     static constexpr int Q_BYTES = RT * KS * 2 * 64 * 16;     // Q^T operands (hi, lo) per workgroup
     static constexpr int OREGS = RT * DT * 4;                 // f32 O^T values per lane
     static constexpr int MERGE_SLOT = (OREGS + 2 * RT) * 64 * 4;
-    static constexpr int MAIN_BYTES = (4 * VT_WAVE > 2 * MERGE_SLOT) ? 4 * VT_WAVE : 2 * MERGE_SLOT;
+    static constexpr int MAIN_BYTES = (NW * VT_WAVE > (NW / 2) * MERGE_SLOT) ? NW * VT_WAVE : (NW / 2) * MERGE_SLOT;
     static constexpr int LDS_BYTES = MAIN_BYTES + Q_BYTES;
     static_assert(VB >= 1 && (KEYS / 4) * (HD / 8) % 64 == 0, "V staging");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
@@ -79,10 +80,11 @@ __device__ __forceinline__ u32x4 buf_load16_nt(rsrc_t r, uint32_t byte_off)
 }
 
 template <int HD, int RT, bool Q_F32, bool O_F32, bool EXT>
-__global__ void __launch_bounds__(kDecodeThreads, decode_waves_per_simd(HD, RT))
+__global__ void __launch_bounds__(64 * decode_waves(HD, RT), decode_waves_per_simd(HD, RT))
 decode_part_kernel(DecodeArgs a)
 {
     using L = DecodeLayout<HD, RT>;
+    constexpr int NW = L::NW;
     constexpr int KS = L::KS, DT = L::DT, VB = L::VB;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -151,7 +153,7 @@ decode_part_kernel(DecodeArgs a)
     const int s_begin = a.k_begin + split * a.chunk;
     const int s_end = min(s_begin + a.chunk, a.k_end);
     const int n_sub = s_begin < s_end ? (s_end - s_begin + L::KEYS - 1) / L::KEYS : 0;
-    const int n_my = n_sub > wave ? (n_sub - wave + 3) / 4 : 0;     // steps wave, wave+4, ...
+    const int n_my = n_sub > wave ? (n_sub - wave + NW - 1) / NW : 0;   // steps wave, wave+NW, ...
 
     // K/V of this kv head; the descriptors end at this split's last key
     const uint32_t kv_bytes = (uint32_t)max(s_end, 0) * HD * 2;
@@ -173,7 +175,7 @@ decode_part_kernel(DecodeArgs a)
     constexpr int DEPTH = L::DEPTH;
     u32x4 kb[DEPTH][2 * KS];
     u32x4 vb[DEPTH][VB][4];
-    auto key0_of = [&](int s) { return s_begin + L::KEYS * (wave + 4 * s); };
+    auto key0_of = [&](int s) { return s_begin + L::KEYS * (wave + NW * s); };
     // K and V of step s into register buffer B (loads past the split read as zero)
     auto issue = [&](auto B, int s) {
         constexpr int b = DEPTH == 2 ? decltype(B)::value : 0;
@@ -318,15 +320,14 @@ decode_part_kernel(DecodeArgs a)
         step(I1{}, s + 1);
     }
 
-    // ---- row sums across the four lanes of a row, then merge the 4 waves in LDS
+    // ---- row sums across the four lanes of a row, then merge the NW waves in LDS (a tree:
+    // the upper half of the waves hands its (O, m, l) to the lower half, log2 NW times)
     float lt[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         lt[rt] = sum_xor32(sum_xor16(l[rt]));
     }
     __syncthreads();                                       // V^T regions are reused below
-    float* slot0 = (float*)lds;
-    float* slot1 = (float*)(lds + L::MERGE_SLOT);
     auto put = [&](float* sl) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -354,14 +355,14 @@ decode_part_kernel(DecodeArgs a)
             m[rt] = M;
         }
     };
-    if (wave >= 2) put(wave == 2 ? slot0 : slot1);
-    __syncthreads();
-    if (wave < 2) take(wave == 0 ? slot0 : slot1);
-    __syncthreads();
-    if (wave == 1) put(slot0);
-    __syncthreads();
+#pragma unroll
+    for (int half = NW / 2; half >= 1; half /= 2) {
+        if (wave >= half && wave < 2 * half) put((float*)(lds + (wave - half) * L::MERGE_SLOT));
+        __syncthreads();
+        if (wave < half) take((const float*)(lds + wave * L::MERGE_SLOT));
+        if (half > 1) __syncthreads();                     // slots are rewritten next level
+    }
     if (wave != 0) return;
-    take(slot0);
 
     // ---- wave 0: lane (row n, group g) holds dims 16*dt + 4*g + (0..3) of its rows
 #pragma unroll
@@ -513,7 +514,7 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int n_rowgroups, hipStrea
         attr_done = true;
     }
     hipLaunchKernelGGL((decode_part_kernel<HD, RT, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
-                       dim3(kDecodeThreads), lds_bytes, stream, a);
+                       dim3(64 * DecodeLayout<HD, RT>::NW), lds_bytes, stream, a);
     return hipGetLastError();
 }
 

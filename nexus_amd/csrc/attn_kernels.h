@@ -17,6 +17,12 @@ constexpr int kWideRowsPerWave = 32;
 // Split-KV decode: 4 waves per (split, kv head, row group), 32 keys per wave step,
 // 16 query rows (n_query * G) per row tile and one or two row tiles per row group.
 constexpr int kDecodeThreads = 256;
+// Waves per decode workgroup: 8 for head dims of 192 and 256, where one workgroup per CU
+// (the host's split rule there) then keeps two waves per SIMD streaming, and a workgroup's
+// fixed cost -- Q staging, the cross-wave merge, the partial -- is shared by twice the keys;
+// 4 below (two workgroups per CU).
+// (The host uses one row tile above head dim 128.)
+constexpr int decode_waves(int head_dim, int row_tiles) { return head_dim >= 192 && row_tiles == 1 ? 8 : 4; }
 constexpr int kDecodeKeys = 32;
 constexpr int kDecodeRowTile = 16;
 constexpr int kDecodeMaxRowTiles = 2;
