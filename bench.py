@@ -344,11 +344,12 @@ def main() -> int:
         measure(args.only, args.steps, args.warmup)
         return 0
 
+    # cfg3 (about 10 ms of GPU work) runs first: the headline is then timed on a GPU whose
+    # clocks have left idle, as in any serving process, instead of in its first milliseconds
+    extra = {"cfg3": measure("cfg3", max(5, args.steps // 5), max(args.warmup, 20))}
     head = measure("cfg2", args.steps, args.warmup)
-    extra = {}
-    for name in ("cfg3", "cfg4", "cfg1", "cfg5"):
-        steps = max(5, args.steps // 5) if name == "cfg3" else args.steps
-        extra[name] = measure(name, steps, args.warmup)
+    for name in ("cfg4", "cfg1", "cfg5"):
+        extra[name] = measure(name, args.steps, args.warmup)
     extra["cfg1_graph"] = measure("cfg1", args.steps, args.warmup, graph=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
 
