@@ -122,19 +122,63 @@ __device__ __forceinline__ void static_for(F&& f)
 constexpr int kWideVAhead = 2;
 constexpr int kWideKAhead = 4;
 
+// Head dim 256: a 32-row wave's O (128 registers) and Q^T operands (64) do not fit two waves
+// per SIMD, so the kernel runs one wave per SIMD with both held in AGPRs -- MFMAs take C/D and
+// A/B from AGPRs, the VALU does not -- which is the only allocation in which the compiler does
+// not shuttle accumulators between the two register files.  Those MFMAs are inline asm with
+// AGPR operand constraints, and the hazard waits the compiler would insert for them are
+// written here (gfx950): two wait states before each MFMA (for a VALU or AGPR write of one of
+// its operands just before it), and 20 (> 18 for a 16-pass 32x32 MFMA) between the last MFMA
+// writing a result and the first VALU access to it, tied to every register of the result.
+template <int HD>
+constexpr bool wide_agpr() { return HD > 128; }
+//   O^T += A B, accumulator in AGPRs
+__device__ __forceinline__ void mfma_acc(f32x16& acc, f16x8 a, f16x8 b)
+{
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+//   S^T = A B + C, B (Q^T) in AGPRs, S in VGPRs
+template <bool FIRST>
+__device__ __forceinline__ void mfma_s(f32x16& d, f16x8 a, const f16x8& b, const f32x16& c0)
+{
+    if constexpr (FIRST)
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "a"(b), "v"(c0));
+    else
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b));
+}
+template <int N1, int N2>
+__device__ __forceinline__ void acc_settle(f32x16 (&x)[N1][N2])
+{
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+a"(x[0][0]));
+#pragma unroll
+    for (int i = 0; i < N1; ++i)
+#pragma unroll
+        for (int j = 0; j < N2; ++j) asm volatile("" : "+a"(x[i][j]));
+}
+template <int N1, int N2>
+__device__ __forceinline__ void s_settle(f32x16 (&x)[N1][N2])
+{
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(x[0][0]));
+#pragma unroll
+    for (int i = 0; i < N1; ++i)
+#pragma unroll
+        for (int j = 0; j < N2; ++j) asm volatile("" : "+v"(x[i][j]));
+}
+
 // s_waitcnt vmcnt(n) (expcnt and lgkmcnt left at their maxima)
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
 
 }  // namespace
 
 template <int HD, int KS, bool Q_F32, bool O_F32>
-__global__ void __launch_bounds__(kPrefillThreads, kWideRowsPerWave == 32 ? 2 : 1)
+__global__ void __launch_bounds__(kPrefillThreads, kWideRowsPerWave == 32 && !wide_agpr<HD>() ? 2 : 1)
 prefill_wide_kernel(PrefillArgs a)
 {
     using L = WideLayout<HD, KS>;
     constexpr int BN = L::BN, SB = L::SB, NB = L::NB, BM = L::BM;
     constexpr int KSTEPS = HD / 16, DBLK = HD / 32;
     constexpr int RPW = kWideRowsPerWave;
+    constexpr bool kAgpr = wide_agpr<HD>();               // O and Q^T in AGPRs (asm MFMAs)
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     lds_u8* lds3 = (lds_u8*)lds;
 
@@ -178,15 +222,18 @@ prefill_wide_kernel(PrefillArgs a)
     const uint32_t kv_bytes = (uint32_t)a.n_ctx * HD * 2;
     const rsrc_t krs = make_rsrc_uniform(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     const rsrc_t vrs = make_rsrc_uniform(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
-    // The swizzle depends on the row only modulo 16, and load j + 1 lands 4096 bytes (a
-    // multiple of 16 rows) after load j, so one per-lane offset serves every load (load j
-    // adds 4096 j).
-    static_assert((kPrefillThreads * 16 / L::ROW) % 16 == 0, "swizzle period");
-    uint32_t koff, voff;
+    // The K swizzle depends on the row modulo 16 and the V swizzle on the row modulo 4 (or
+    // 2), and load j + 1 lands 4096 bytes after load j: 16 or more rows at head dim <= 128,
+    // so one per-lane offset serves every load (load j adds 4096 j); 8 rows at head dim 256,
+    // where loads of odd j take the K offset of the row 8 further on.
+    constexpr int RPL = kPrefillThreads * 16 / L::ROW;    // rows per load
+    static_assert(RPL % 16 == 0 || RPL == 8, "swizzle period");
+    uint32_t koff[2], voff;
     {
         const int b = 16 * tid;
         const int row = b / L::ROW, slot = (b % L::ROW) / 16;
-        koff = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row, slot));
+        koff[0] = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row, slot));
+        koff[1] = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row + RPL, slot));
         voff = (uint32_t)(row * L::ROW + 16 * wv_slot<HD>(row, slot));
     }
     // tiles of step `st`: tile st * KS + i goes to slot (st % 2) * KS + i.  Loads past the cache
@@ -207,7 +254,7 @@ prefill_wide_kernel(PrefillArgs a)
                 // (zeros past the cache end) covers it
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     k_side ? krs : vrs, (void __attribute__((address_space(3)))*)(dst + 4096 * j), 16,
-                    (int)(k_side ? koff : voff) + base + 4096 * j, 0, 0, 0);
+                    (int)(k_side ? koff[RPL == 8 ? (j & 1) : 0] : voff) + base + 4096 * j, 0, 0, 0);
         }
     };
     // group st: what step st consumes, K(st + 1) and V(st)
@@ -268,6 +315,7 @@ prefill_wide_kernel(PrefillArgs a)
             const float qs = a.scale_log2;
             qt[rb][ks] = cvt_f16x8(x[0] * qs, x[1] * qs, x[2] * qs, x[3] * qs, x[4] * qs, x[5] * qs,
                                    x[6] * qs, x[7] * qs);
+            if constexpr (kAgpr) asm volatile("" : "+a"(qt[rb][ks]));    // its home: AGPRs
         }
 
     // ---- per-lane LDS read offsets within a tile
@@ -303,6 +351,9 @@ prefill_wide_kernel(PrefillArgs a)
         for (int db = 0; db < DBLK; ++db)
 #pragma unroll
             for (int v = 0; v < 16; ++v) o[rb][db][v] = 0.f;
+        if constexpr (kAgpr)
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) asm volatile("" : "+a"(o[rb][db]));
 #pragma unroll
         for (int v = 0; v < 16; ++v) negm[rb][v] = 0.f;
         m_used[rb] = 0.f;
@@ -327,8 +378,12 @@ prefill_wide_kernel(PrefillArgs a)
             u32x4 ka = ds_read_b128<32 * sb * L::ROW>(lds3 + ka_off[ks]);
             wait_lgkm<0>(ka);
 #pragma unroll
-            for (int rb = 0; rb < NB; ++rb)
-                sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+            for (int rb = 0; rb < NB; ++rb) {
+                if constexpr (kAgpr)
+                    mfma_s<ks == 0>(sn[rb][sb], __builtin_bit_cast(f16x8, ka), qt[rb][ks], negm[rb]);
+                else
+                    sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+            }
         });
     };
     // causal / cache-end mask of tile t; wave-uniform test (diagonal and last tiles)
@@ -365,6 +420,7 @@ prefill_wide_kernel(PrefillArgs a)
             any_need = any_need || need[rb];
         }
         if (__any(any_need)) {
+            if constexpr (kAgpr) acc_settle(o);
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
                 const float d = need[rb] ? mx[rb] : 0.f;
@@ -373,7 +429,10 @@ prefill_wide_kernel(PrefillArgs a)
                 seen[rb] = seen[rb] || need[rb];
                 l_part[rb] *= corr;
 #pragma unroll
-                for (int db = 0; db < DBLK; ++db) o[rb][db] *= corr;
+                for (int db = 0; db < DBLK; ++db) {
+                    o[rb][db] *= corr;
+                    if constexpr (kAgpr) asm volatile("" : "+a"(o[rb][db]));
+                }
 #pragma unroll
                 for (int sb = 0; sb < SB; ++sb) sv[rb][sb] -= d;
 #pragma unroll
@@ -408,7 +467,9 @@ prefill_wide_kernel(PrefillArgs a)
     };
     constexpr int KITER = KSTEPS * SB;                   // K operand reads per tile
     constexpr int PELEMS = NB * SB * 16;                 // score elements per lane per tile
-    static_assert(PELEMS % (2 * KITER) == 0, "P pairs per K step");
+    // the P work (score pairs) is spread over the K MFMA slots and the row-max work over the
+    // PV groups: slot i of n takes pairs [i * PAIRS / n, (i + 1) * PAIRS / n)
+    constexpr int PAIRS = PELEMS / 2;
 
     // Phase A of a step: S^T(next) = K Q^T - m on the MFMAs, with P(t) on the VALU.  The
     // program order below is the issue order (sched_barrier between slices): K reads run
@@ -430,11 +491,14 @@ prefill_wide_kernel(PrefillArgs a)
             constexpr int LATER = (KITER - 1 - i) < AHEAD ? (KITER - 1 - i) : AHEAD;
             wait_lgkm<LATER>(ka[i]);
 #pragma unroll
-            for (int rb = 0; rb < NB; ++rb)
-                sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
-            constexpr int E = PELEMS / KITER;
+            for (int rb = 0; rb < NB; ++rb) {
+                if constexpr (kAgpr)
+                    mfma_s<ks == 0>(sn[rb][sb], __builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], negm[rb]);
+                else
+                    sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+            }
 #pragma unroll
-            for (int e = i * E; e < (i + 1) * E; e += 2) p_pair(sc, pw, e);
+            for (int pr = i * PAIRS / KITER; pr < (i + 1) * PAIRS / KITER; ++pr) p_pair(sc, pw, 2 * pr);
             __builtin_amdgcn_sched_barrier(0);
         });
     };
@@ -462,7 +526,12 @@ prefill_wide_kernel(PrefillArgs a)
             wait_lgkm<2 * LATER>(vr[gv][0], vr[gv][1]);
             const f16x8 va = __builtin_bit_cast(f16x8, u32x4{vr[gv][0][0], vr[gv][0][1], vr[gv][1][0], vr[gv][1][1]});
 #pragma unroll
-            for (int rb = 0; rb < NB; ++rb) o[rb][db] = mfma32x32x16(va, p_operand(pw, rb, sb, j), o[rb][db]);
+            for (int rb = 0; rb < NB; ++rb) {
+                if constexpr (kAgpr)
+                    mfma_acc(o[rb][db], va, p_operand(pw, rb, sb, j));
+                else
+                    o[rb][db] = mfma32x32x16(va, p_operand(pw, rb, sb, j), o[rb][db]);
+            }
             between(GV);
             __builtin_amdgcn_sched_barrier(0);
         });
@@ -495,6 +564,7 @@ prefill_wide_kernel(PrefillArgs a)
         PTile pw;
         // phase A: S(tn) MFMAs, P(t) on the VALU
         phase_a(std::integral_constant<int, par ^ 1>{}, sc, sn, pw);
+        if constexpr (kAgpr) s_settle(sn);                 // S(tn) is read by the VALU below
         __builtin_amdgcn_s_setprio(2);
         // phase B: PV(t) MFMAs, row max of S(tn) on the VALU (running max3 over element pairs)
         STile& sx = kSCopy ? sc : sn;
@@ -503,9 +573,9 @@ prefill_wide_kernel(PrefillArgs a)
         for (int rb = 0; rb < NB; ++rb) mrun[rb] = -INFINITY;
         pv_tile(PAR, pw, [&](auto GV) {
             constexpr int gv = decltype(GV)::value;
-            constexpr int M = PELEMS / VGROUPS;
 #pragma unroll
-            for (int e = gv * M; e < (gv + 1) * M; e += 2) {
+            for (int pr = gv * PAIRS / VGROUPS; pr < (gv + 1) * PAIRS / VGROUPS; ++pr) {
+                const int e = 2 * pr;
                 const int rb = e / (SB * 16), sb = (e / 16) % SB, v = e % 16;
                 if constexpr (kSCopy) {
                     sc[rb][sb][v] = sn[rb][sb][v];
@@ -536,12 +606,14 @@ prefill_wide_kernel(PrefillArgs a)
         {
             if constexpr (kSCopy) {
                 s_tile(sB);
+                if constexpr (kAgpr) s_settle(sB);
 #pragma unroll
                 for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
                     for (int sb = 0; sb < SB; ++sb) sA[rb][sb] = sB[rb][sb];
             } else {
                 s_tile(sA);
+                if constexpr (kAgpr) s_settle(sA);
             }
             float mx[NB];
 #pragma unroll
@@ -579,6 +651,7 @@ prefill_wide_kernel(PrefillArgs a)
     // the loads past the end are still in flight: none may land in LDS after this point
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_s_waitcnt(wait_vm(0));
+    if constexpr (kAgpr) acc_settle(o);
 
     // ---- epilogue
     float l_tot[NB], m_out[NB];
@@ -702,7 +775,7 @@ static hipError_t launch_wide_ks(const PrefillArgs& a, bool q_f32, bool o_f32, h
     return o_f32 ? launch_wide_t<HD, KS, false, true>(a, s) : launch_wide_t<HD, KS, false, false>(a, s);
 }
 
-bool prefill_wide_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
+bool prefill_wide_supported(int head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 
 hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32,
                                hipStream_t stream)
@@ -711,6 +784,7 @@ hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool 
     switch (head_dim) {
     case 64: return ks == 1 ? launch_wide_ks<64, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<64, 2>(a, q_f32, o_f32, stream);
     case 128: return ks == 1 ? launch_wide_ks<128, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<128, 2>(a, q_f32, o_f32, stream);
+    case 256: return ks == 1 ? launch_wide_ks<256, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<256, 2>(a, q_f32, o_f32, stream);
     default: return hipErrorInvalidValue;
     }
 }

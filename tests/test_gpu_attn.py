@@ -79,6 +79,13 @@ PREFILL_CASES = [
     (64, 16, 64, 512, 0, 0, True, True, 0, 0.0),       # hd 64
     # pipelined kernel, 64-row blocks, odd tile count: key group 1 runs one tile past the end
     (8, 2, 128, 80, 0, 0, True, False, 0, 0.0),
+    # pipelined kernel at head dim 256 (one wave per SIMD, O and Q^T in AGPRs): >= 256 blocks
+    (64, 8, 256, 512, 0, 0, True, True, 0, 0.0),      # cold
+    (32, 4, 256, 1030, 17, 5, False, False, 0, 0.0),  # f32 q/o, ragged last block, padded stride
+    (32, 4, 256, 1024, 300, 0, True, False, 0, 0.0),  # chunk after a cache, f32 out
+    # head dim 256 with fewer blocks than CUs stays on prefill_kernel
+    (16, 2, 256, 1030, 0, 0, True, True, 0, 0.0),
+    (16, 4, 256, 64, 500, 0, True, False, 0, 0.0),
 ]
 
 
@@ -280,9 +287,9 @@ def _sample_rows(nq, hq, n, seed):
     return np.unique(np.concatenate([rows, [0, hq - 1, nq * hq - 1, (nq - 1) * hq]])).astype(np.int32)
 
 
-@pytest.mark.parametrize("cfg", ["cfg2", "cfg3"])
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg3", "q35"])
 def test_prefill_full_config_sampled_rows(hip, cfg):
-    hq, hkv, hd = 40, 8, 128
+    hq, hkv, hd = (16, 2, 256) if cfg == "q35" else (40, 8, 128)
     nq, base = (512, 4096) if cfg == "cfg2" else (8192, 0)
     n_ctx = base + nq
     print(f"[case] {cfg} full size", flush=True)
