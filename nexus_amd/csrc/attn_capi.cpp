@@ -220,10 +220,9 @@ PrefillPlan prefill_plan(const nexus_attn_desc* d)
         const long long rows1 = nxa::prefill_wide_rows(1);
         const long long wgs1 = (long long)d->n_q_heads * ((d->n_query + rows1 - 1) / rows1);
         const bool few = wgs1 < device_cus();
-        // Head dim 256 runs the pipelined kernel in its 128-row form only: its two-key-group
-        // form returned zeros in one 16-dim slice of O (an accumulator-tuple problem in the
-        // AGPR epilogue, found by the parity tests and not yet resolved), so short head-256
-        // prompts keep prefill_kernel.
+        // Head dim 256 runs the pipelined kernel in its 128-row form only (the two-key-group
+        // form does not fit one wave per SIMD's registers), so short head-256 prompts keep
+        // prefill_kernel.
         if (!(few && d->head_dim == 256)) {
             p.wide = true;
             p.ks = few ? 2 : 1;

@@ -146,6 +146,11 @@ __device__ __forceinline__ void mfma_s(f32x16& d, f16x8 a, const f16x8& b, const
     else
         asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b));
 }
+//   S^T = A B (no bias), B in AGPRs
+__device__ __forceinline__ void mfma_s_zero(f32x16& d, f16x8 a, const f16x8& b)
+{
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b));
+}
 template <int N1, int N2>
 __device__ __forceinline__ void acc_settle(f32x16 (&x)[N1][N2])
 {
@@ -163,6 +168,18 @@ __device__ __forceinline__ void s_settle(f32x16 (&x)[N1][N2])
     for (int i = 0; i < N1; ++i)
 #pragma unroll
         for (int j = 0; j < N2; ++j) asm volatile("" : "+v"(x[i][j]));
+}
+
+// The bias (SrcC) of the first S MFMA of a tile is read by the MFMA over its passes: its
+// registers must not be rewritten (a VALU result, an LDS read landing) until the MFMA is done.
+// A use after the settle keeps them allocated until then.
+template <int N>
+__device__ __forceinline__ void keep_bias(const f32x16 (&x)[N])
+{
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(x[i][v]));   // per element: the host pass has no 64-byte "v" operand
 }
 
 // s_waitcnt vmcnt(n) (expcnt and lgkmcnt left at their maxima)
@@ -379,8 +396,10 @@ prefill_wide_kernel(PrefillArgs a)
             wait_lgkm<0>(ka);
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
-                if constexpr (kAgpr)
-                    mfma_s<ks == 0>(sn[rb][sb], __builtin_bit_cast(f16x8, ka), qt[rb][ks], negm[rb]);
+                if constexpr (kAgpr && ks == 0)
+                    mfma_s_zero(sn[rb][sb], __builtin_bit_cast(f16x8, ka), qt[rb][ks]);   // m = 0 here
+                else if constexpr (kAgpr)
+                    mfma_s<false>(sn[rb][sb], __builtin_bit_cast(f16x8, ka), qt[rb][ks], negm[rb]);
                 else
                     sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
             }
@@ -564,7 +583,10 @@ prefill_wide_kernel(PrefillArgs a)
         PTile pw;
         // phase A: S(tn) MFMAs, P(t) on the VALU
         phase_a(std::integral_constant<int, par ^ 1>{}, sc, sn, pw);
-        if constexpr (kAgpr) s_settle(sn);                 // S(tn) is read by the VALU below
+        if constexpr (kAgpr) {
+            s_settle(sn);                                  // S(tn) is read by the VALU below
+            keep_bias(negm);
+        }
         __builtin_amdgcn_s_setprio(2);
         // phase B: PV(t) MFMAs, row max of S(tn) on the VALU (running max3 over element pairs)
         STile& sx = kSCopy ? sc : sn;
@@ -597,6 +619,9 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
         for (int e = 0; e < PELEMS; e += 2) p_pair(sc, pw, e);
         pv_tile(PAR, pw, [](auto) {});
+        // the paths into the epilogue join here: the compiler's register copies that join
+        // them come after this wait
+        if constexpr (kAgpr) acc_settle(o);
     };
 
     if (n_steps > 0) {                                     // workgroup-uniform: empty split
@@ -784,7 +809,10 @@ hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool 
     switch (head_dim) {
     case 64: return ks == 1 ? launch_wide_ks<64, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<64, 2>(a, q_f32, o_f32, stream);
     case 128: return ks == 1 ? launch_wide_ks<128, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<128, 2>(a, q_f32, o_f32, stream);
-    case 256: return ks == 1 ? launch_wide_ks<256, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<256, 2>(a, q_f32, o_f32, stream);
+    // head dim 256: 128-row blocks only.  Two key groups per workgroup need more registers
+    // than one wave per SIMD has (the merge and the second group's state); the compiler then
+    // moves accumulator blocks between register files right beside the inline-asm MFMAs.
+    case 256: return ks == 1 ? launch_wide_ks<256, 1>(a, q_f32, o_f32, stream) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }
