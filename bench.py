@@ -27,6 +27,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 MALL_BYTES = 256 << 20
+WARM_S = 0.03                    # minimum warm-up time per measured config
 
 METRIC = "attn prefill TFLOP/s (% MFMA peak) + decode KV GB/s (% HBM peak), 1 MI355X"
 
@@ -39,6 +40,8 @@ CONFIGS = {
                  desc="cold prefill 8192 tokens, 40q/8kv, hd128, f16 Q/K/V/O, f32 softmax stats"),
     "cfg4": dict(kind="decode", hq=40, hkv=8, hd=128, nq=1, base=61439, n_ctx=61440, q="f32", o="f32", splits=64,
                  desc="decode 1 token, 40q/8kv, hd128, 61440 keys, 64 splits, f32 LSE combine"),
+    "q35p": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=8192, base=0, n_ctx=8192, q="f16", o="f16",
+                 desc="cold prefill 8192 tokens, 16q/2kv, hd256 (the Qwen3.5 full-attention layer's shape)"),
     "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
                  desc="MTP verify 4 drafts at 32768 cached tokens, 16q/2kv, hd256, causal among drafts"),
 }
@@ -55,6 +58,22 @@ def work_of(c: dict) -> tuple[float, str]:
         return capi.prefill_flops(c["hq"], c["hd"], c["nq"], c["base"], c["n_ctx"]), "flop"
     n_keys = min(c["base"] + c["nq"] - 1, c["n_ctx"] - 1) + 1
     return capi.decode_bytes(c["hkv"], c["hd"], n_keys, c["hq"], c["nq"]), "byte"
+
+
+def warm_up(call, warmup: int, min_s: float = WARM_S) -> None:
+    """At least `warmup` untimed calls, and more until `min_s` seconds of back-to-back work have
+    passed: the GPU's clocks settle under sustained load of the kind timed next (measured on
+    MI355X: cfg2 launches take ~70 us in the first milliseconds after idle, ~62-66 us later)."""
+    import torch
+
+    t_end = time.perf_counter() + min_s
+    i = 0
+    while i < warmup or time.perf_counter() < t_end:
+        call(i)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
 
 
 def measure(name: str, steps: int, warmup: int, graph: bool = False) -> dict:
@@ -100,9 +119,7 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False) -> dict:
             capi.prefill_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr(),
                              ws_bytes, stream)
 
-    for i in range(warmup):
-        call(i)
-    torch.cuda.synchronize()
+    warm_up(call, warmup)
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if graph:
         gr = torch.cuda.CUDAGraph()
@@ -192,9 +209,7 @@ def measure_decode_layer(steps: int, warmup: int) -> dict:
 
     def timed(fn):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        for i in range(warmup):
-            fn(i, stream)
-        torch.cuda.synchronize()
+        warm_up(lambda i: fn(i, stream), warmup)
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
             cap_stream = torch.cuda.current_stream(dev).cuda_stream
@@ -344,13 +359,12 @@ def main() -> int:
         measure(args.only, args.steps, args.warmup)
         return 0
 
-    # cfg3 (about 10 ms of GPU work) runs first: the headline is then timed on a GPU whose
-    # clocks have left idle, as in any serving process, instead of in its first milliseconds
     extra = {"cfg3": measure("cfg3", max(5, args.steps // 5), max(args.warmup, 20))}
     head = measure("cfg2", args.steps, args.warmup)
     for name in ("cfg4", "cfg1", "cfg5"):
         extra[name] = measure(name, args.steps, args.warmup)
     extra["cfg1_graph"] = measure("cfg1", args.steps, args.warmup, graph=True)
+    extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
 
     cpu = None
