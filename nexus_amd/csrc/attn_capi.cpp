@@ -183,15 +183,14 @@ size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
     return nxa::ws_partial_bytes((long long)d->n_query * d->n_q_heads, splits, d->head_dim);
 }
 
-// Split count of the prefill kernel.  Splitting costs a partial write + read per row and
-// split plus a combine launch, which only pays off when the unsplit grid leaves most CUs
-// idle (measured on MI355X: 160 workgroups of 512 queries x 40 heads run faster unsplit
-// than in 3 splits).  Below half a workgroup per CU, split so the grid reaches about one
-// workgroup per CU, each split keeping >= 4 key tiles.
-int prefill_splits(const nexus_attn_desc* d)
+// Split count of a prefill grid of `base` query-block workgroups.  Splitting costs a partial
+// write + read per row and split plus a combine launch, which only pays off when the unsplit
+// grid leaves most CUs idle (measured on MI355X: 160 workgroups of 512 queries x 40 heads run
+// faster unsplit than in 3 splits; 320 pipelined workgroups of 64 queries x 40 heads in 2
+// splits take 96 us against 62 unsplit).  Below half a workgroup per CU, split so the grid
+// reaches about one workgroup per CU, each split keeping >= 4 key tiles of 64.
+int prefill_splits(const nexus_attn_desc* d, long long base)
 {
-    const long long qblocks = (d->n_query + nxa::kPrefillBM - 1) / nxa::kPrefillBM;
-    const long long base = qblocks * d->n_q_heads;
     const long long cus = device_cus();
     if (2 * base >= cus) return 1;
     long long s = cus / base;
@@ -204,32 +203,33 @@ int prefill_splits(const nexus_attn_desc* d)
 }
 
 // Prefill kernel choice.  Plain causal shapes (no softcap, no sliding window) at the head
-// dims the pipelined kernel covers take it, unsplit: 128-row blocks (KS = 1), or 64-row
-// blocks with the key range split over two waves of the workgroup (KS = 2) when 128-row
-// blocks leave CUs without a workgroup.  Other shapes take prefill_kernel with its split rule.
+// dims the pipelined kernel covers take it: 128-row blocks (KS = 1), or 64-row blocks with
+// the key range split over two waves of the workgroup (KS = 2) when 128-row blocks leave
+// CUs without a workgroup (head dim 256 has the 128-row form only: the two-key-group form
+// does not fit one wave per SIMD's registers).  Either grid splits the key range over
+// workgroups by the rule above.  Other shapes take prefill_kernel with the same rule.
 struct PrefillPlan {
     bool wide;
     int ks;
     int splits;
 };
 
+long long query_blocks(const nexus_attn_desc* d, long long rows)
+{
+    return (long long)d->n_q_heads * ((d->n_query + rows - 1) / rows);
+}
+
 PrefillPlan prefill_plan(const nexus_attn_desc* d)
 {
     PrefillPlan p{false, 1, 1};
     if (!is_ext(d) && nxa::prefill_wide_supported(d->head_dim)) {
-        const long long rows1 = nxa::prefill_wide_rows(1);
-        const long long wgs1 = (long long)d->n_q_heads * ((d->n_query + rows1 - 1) / rows1);
-        const bool few = wgs1 < device_cus();
-        // Head dim 256 runs the pipelined kernel in its 128-row form only (the two-key-group
-        // form does not fit one wave per SIMD's registers), so short head-256 prompts keep
-        // prefill_kernel.
-        if (!(few && d->head_dim == 256)) {
-            p.wide = true;
-            p.ks = few ? 2 : 1;
-            return p;
-        }
+        const bool few = query_blocks(d, nxa::prefill_wide_rows(1)) < device_cus();
+        p.wide = true;
+        p.ks = few && d->head_dim != 256 ? 2 : 1;
+        p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks)));
+        return p;
     }
-    p.splits = prefill_splits(d);
+    p.splits = prefill_splits(d, query_blocks(d, nxa::kPrefillBM));
     return p;
 }
 

@@ -483,10 +483,80 @@ combine_kernel(CombineArgs a)
     }
 }
 
+// The same merge for many rows with few splits (split prefill): one wave per row, four rows
+// per workgroup, lane l folding every split of dim pairs l, l + 64, ...; a batch of 8 splits
+// is one memory round trip.  The one-workgroup-per-row kernel above spends its time on
+// workgroup dispatch there (20480 rows x 2 splits: 37.8 us).
+constexpr int kCombineRowsWaves = 4;
+
+template <int HD, bool O_F32>
+__global__ void __launch_bounds__(64 * kCombineRowsWaves)
+combine_rows_kernel(CombineArgs a)
+{
+    constexpr int DP = HD / 2, PPL = (DP + 63) / 64, BATCH = 8;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kCombineRowsWaves + (int)(threadIdx.x >> 6);
+    if (row >= a.n_rows) return;
+    const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
+
+    float M = kNegBig * 4.f, L = 0.f;               // below any partial's m (kNegBig)
+    f32x2 acc[PPL];
+#pragma unroll
+    for (int p = 0; p < PPL; ++p) acc[p] = f32x2{0.f, 0.f};
+    for (int c0 = 0; c0 < a.n_splits; c0 += BATCH) {
+        f32x2 x[BATCH][PPL], ml[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const int c = c0 + j;
+            const bool ok = c < a.n_splits;
+            const float* ps = pr + (size_t)(ok ? c : 0) * (HD + 2);
+#pragma unroll
+            for (int p = 0; p < PPL; ++p) {
+                const int d = lane + 64 * p;
+                x[j][p] = (ok && d < DP) ? *(const f32x2*)(ps + 2 * d) : f32x2{0.f, 0.f};
+            }
+            ml[j] = ok ? *(const f32x2*)(ps + HD) : f32x2{kNegBig * 4.f, 0.f};
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) Mb = fmaxf(Mb, ml[j][0]);
+        const float cr = fast_exp2((M - Mb) * kLog2e);
+        L *= cr;
+#pragma unroll
+        for (int p = 0; p < PPL; ++p) acc[p] *= cr;
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const float w = fast_exp2((ml[j][0] - Mb) * kLog2e);
+            L += ml[j][1] * w;
+#pragma unroll
+            for (int p = 0; p < PPL; ++p) acc[p] += x[j][p] * w;
+        }
+        M = Mb;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int p = 0; p < PPL; ++p) {
+        const int d = lane + 64 * p;
+        if (d >= DP) continue;
+        const f32x2 y = acc[p] * inv * gate2(a.gate, (size_t)row * HD + 2 * d);
+        if constexpr (O_F32) {
+            *(f32x2*)((float*)a.out + (size_t)row * HD + 2 * d) = y;
+        } else {
+            const f16x2 hy = __builtin_convertvector(y, f16x2);
+            *(f16x2*)((_Float16*)a.out + (size_t)row * HD + 2 * d) = hy;
+        }
+    }
+}
+
 template <int HD, bool OF>
 static hipError_t launch_combine_t(const CombineArgs& a, hipStream_t stream)
 {
-    hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows), dim3(CombineLayout<HD>::THREADS), 0, stream, a);
+    if (combine_by_rows(a.n_rows, a.n_splits)) {
+        const int wgs = (a.n_rows + kCombineRowsWaves - 1) / kCombineRowsWaves;
+        hipLaunchKernelGGL((combine_rows_kernel<HD, OF>), dim3(wgs), dim3(64 * kCombineRowsWaves), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows), dim3(CombineLayout<HD>::THREADS), 0, stream, a);
+    }
     return hipGetLastError();
 }
 

@@ -119,6 +119,9 @@ hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool 
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);
 hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream);
+// Which combine kernel runs: one wave per row for many rows with few splits (split prefill),
+// one workgroup per row otherwise (decode: tens of rows, up to 256 splits).
+constexpr bool combine_by_rows(int n_rows, int n_splits) { return n_rows >= 256 && n_splits <= 16; }
 // One workgroup (one wave) per q, k and v head: n_heads + 2 * n_kv workgroups.
 hipError_t launch_decode_prep(const PrepArgs& a, hipStream_t stream);
 

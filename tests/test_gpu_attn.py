@@ -72,7 +72,7 @@ PREFILL_CASES = [
     (6, 2, 192, 70, 10, 0, True, True, 0, 0.0),        # hd 192
     (8, 8, 128, 130, 0, 0, True, True, 50, 0.0),       # sliding window
     (8, 4, 128, 100, 60, 0, False, False, 0, 30.0),    # softcap
-    (8, 2, 128, 64, 2000, 0, True, True, 0, 0.0),      # long cache, short chunk (split path)
+    (8, 2, 128, 64, 2000, 0, True, True, 0, 0.0),      # long cache, short chunk: pipelined kernel in 8 key splits
     (40, 8, 128, 33, 1000, 0, True, True, 0, 0.0),     # cfg-2 head layout, small
     # pipelined kernel with 128-row blocks (>= one block per CU of a 256-CU MI355X)
     (64, 8, 128, 520, 37, 3, False, False, 0, 0.0),    # ragged last block, unaligned base, f32 q/o
@@ -83,9 +83,13 @@ PREFILL_CASES = [
     (64, 8, 256, 512, 0, 0, True, True, 0, 0.0),      # cold
     (32, 4, 256, 1030, 17, 5, False, False, 0, 0.0),  # f32 q/o, ragged last block, padded stride
     (32, 4, 256, 1024, 300, 0, True, False, 0, 0.0),  # chunk after a cache, f32 out
-    # head dim 256 with fewer blocks than CUs stays on prefill_kernel
+    # head dim 256 with fewer blocks than CUs: 128-row blocks, unsplit or in key splits
     (16, 2, 256, 1030, 0, 0, True, True, 0, 0.0),
     (16, 4, 256, 64, 500, 0, True, False, 0, 0.0),
+    # key splits merged by the one-wave-per-row combine (>= 256 rows); hd 192 on prefill_kernel
+    (4, 4, 64, 100, 3000, 0, False, False, 0, 0.0),    # 12 splits: a partial second merge batch
+    (8, 1, 256, 64, 4000, 0, True, True, 0, 0.0),      # 16 splits: two full merge batches
+    (6, 2, 192, 70, 2000, 0, True, False, 0, 0.0),
 ]
 
 
@@ -140,7 +144,9 @@ GATED_PREFILL_CASES = [
     # (Hq, Hkv, hd, n_query, q_base, q_f16, o_f16, sw, cap, split) -- one per epilogue
     (64, 8, 128, 520, 37, False, False, 0, 0.0, True),     # pipelined kernel, 128-row blocks, f32 out
     (8, 2, 128, 80, 0, True, True, 0, 0.0, True),          # pipelined kernel, 64-row blocks (key-group merge)
-    (16, 2, 256, 96, 40, True, True, 0, 0.0, True),        # general kernel, hd 256
+    (16, 2, 256, 96, 40, True, True, 0, 0.0, True),        # pipelined kernel, hd 256
+    (8, 2, 128, 64, 2000, True, False, 0, 0.0, True),      # pipelined kernel's key split + row combine
+    (6, 2, 192, 70, 10, True, True, 0, 0.0, True),         # general kernel, hd 192
     (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # general kernel, softcap
     (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # general kernel's key split + combine
 ]
