@@ -42,6 +42,8 @@ CONFIGS = {
                  desc="decode 1 token, 40q/8kv, hd128, 61440 keys, 64 splits, f32 LSE combine"),
     "q35p": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=8192, base=0, n_ctx=8192, q="f16", o="f16",
                  desc="cold prefill 8192 tokens, 16q/2kv, hd256 (the Qwen3.5 full-attention layer's shape)"),
+    "q35c": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=512, base=32768, n_ctx=33280, q="f16", o="f16",
+                 desc="chunked prefill 512 queries after 32768 cached tokens, 16q/2kv, hd256 (key splits + combine)"),
     "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
                  desc="MTP verify 4 drafts at 32768 cached tokens, 16q/2kv, hd256, causal among drafts"),
 }
@@ -365,6 +367,7 @@ def main() -> int:
         extra[name] = measure(name, args.steps, args.warmup)
     extra["cfg1_graph"] = measure("cfg1", args.steps, args.warmup, graph=True)
     extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup)
+    extra["q35c"] = measure("q35c", args.steps, args.warmup)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
 
     cpu = None
