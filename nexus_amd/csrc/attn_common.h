@@ -114,6 +114,15 @@ constexpr uint32_t kSelHi = 0x07060302u;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Softcapped score in log2 units, softcap * tanh(x / softcap) * log2(e), with
+// tanh(y) = 1 - 2 / (e^(2y) + 1) on v_exp_f32 and v_rcp_f32: five VALU operations instead of
+// a division and a library tanh; absolute error of tanh ~1e-7, the +-1 limits exact (e^(2y)
+// overflows to inf or underflows to 0).  c1 = 2 log2(e) / softcap, c2 = softcap log2(e).
+__device__ __forceinline__ float softcap_log2(float x, float c1, float c2)
+{
+    return c2 - 2.f * c2 * __builtin_amdgcn_rcpf(fast_exp2(x * c1) + 1.f);
+}
+
 // Output gate of the gated attention layers: sigmoid(z), clamped to 1 above z = 80 and to 0
 // below -80 (qwen35_attn_comb.comp:34-38; the CPU path, transformer.h:8508-8511).
 __device__ __forceinline__ float gate_sigmoid(float z)

@@ -161,6 +161,7 @@ decode_part_kernel(DecodeArgs a)
     const rsrc_t vrs = make_rsrc_uniform(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     uint8_t* vw = lds + wave * L::VT_WAVE;
     const float fc = EXT ? 1.f : a.scale_log2;
+    const float cap_c1 = a.softcap > 0.f ? 2.f * kLog2e / a.softcap : 0.f, cap_c2 = a.softcap * kLog2e;
 
     // per-lane K rows of the two 16-key tiles: tile t, row n -> key 8*(n/4) + 4t + n%4
     const uint32_t krow0 = 8 * (n >> 2) + (n & 3);
@@ -268,8 +269,7 @@ decode_part_kernel(DecodeArgs a)
                     float x = sc[t][rt][i];
                     if constexpr (EXT) {
                         x *= a.scale;
-                        if (a.softcap > 0.f) x = a.softcap * tanhf(x / a.softcap);
-                        x *= kLog2e;
+                        x = a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e;
                     }
                     const bool vis = rok[rt] && key < s_end && key <= khi[rt] && key >= klo[rt];
                     x = vis ? x : -INFINITY;

@@ -178,6 +178,7 @@ prefill_kernel(PrefillArgs a)
 
     // ---- Q^T operands, pre-scaled: lane (query n, k-group hh) holds dims 16*ks + 8*hh .. +7
     const float qscale = EXT ? a.scale : a.scale_log2;
+    const float cap_c1 = a.softcap > 0.f ? 2.f * kLog2e / a.softcap : 0.f, cap_c2 = a.softcap * kLog2e;
     constexpr uint32_t QE = Q_F32 ? 4u : 2u;
     f16x8 qt[KSTEPS];
     {
@@ -306,9 +307,8 @@ prefill_kernel(PrefillArgs a)
             for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    float x = s[sb][v];
-                    if (a.softcap > 0.f) x = a.softcap * tanhf(x / a.softcap);
-                    s[sb][v] = x * kLog2e - m_used;
+                    const float x = s[sb][v];
+                    s[sb][v] = (a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e) - m_used;
                 }
         }
         if (need_mask) {                                  // wave-uniform: diagonal / boundary tiles
