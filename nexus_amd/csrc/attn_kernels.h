@@ -110,11 +110,11 @@ inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.
 hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                           hipStream_t stream);
-// Wide prefill: plain causal shapes (no softcap, no sliding window, one key split), head dims
-// prefill_wide_supported() accepts; n_qblocks counts prefill_wide_rows(ks)-row blocks.
+// Wide (pipelined) prefill: causal shapes at the head dims prefill_wide_supported() accepts,
+// with softcap and sliding window when `ext`; n_qblocks counts prefill_wide_rows(ks)-row blocks.
 bool prefill_wide_supported(int head_dim);
 int prefill_wide_rows(int ks);
-hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32,
+hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32, bool ext,
                                hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);

@@ -187,7 +187,7 @@ constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
 
 }  // namespace
 
-template <int HD, int KS, bool Q_F32, bool O_F32>
+template <int HD, int KS, bool Q_F32, bool O_F32, bool EXT>
 __global__ void __launch_bounds__(kPrefillThreads, kWideRowsPerWave == 32 && !wide_agpr<HD>() ? 2 : 1)
 prefill_wide_kernel(PrefillArgs a)
 {
@@ -214,14 +214,17 @@ prefill_wide_kernel(PrefillArgs a)
     const int split = r - g * a.n_splits;
     const int h = kvh * a.group + g;
 
-    // ---- key tiles of this workgroup: [t0, t1) of the block's tiles 0 .. k_hi / BN, split
+    // ---- key tiles of this workgroup: [t0, t1) of the block's tiles t_lo .. k_hi / BN, split
     // evenly over n_splits workgroups; keys from kmax on belong to later splits (or past the
-    // cache end) and are masked
+    // cache end) and are masked.  A sliding window starts the range at the tile of the first
+    // row's first key (later rows' earlier keys are masked).
     const int q0 = qb * BM;
     const int k_hi = min(a.q_base + min(q0 + BM, a.n_query) - 1, a.n_ctx - 1);
     const int n_tiles = k_hi / BN + 1;
-    const int tps = (n_tiles + a.n_splits - 1) / a.n_splits;
-    const int t0 = min(split * tps, n_tiles), t1 = min(t0 + tps, n_tiles);
+    const bool swa = EXT && a.sliding_window > 0;
+    const int t_lo = swa ? min(max(0, a.q_base + q0 + 1 - a.sliding_window) / BN, n_tiles) : 0;
+    const int tps = (n_tiles - t_lo + a.n_splits - 1) / a.n_splits;
+    const int t0 = min(t_lo + split * tps, n_tiles), t1 = min(t0 + tps, n_tiles);
     const int kmax = min(a.n_ctx, t1 * BN);
     const int n_steps = (t1 - t0 + KS - 1) / KS;         // 0 for an empty split
 
@@ -329,7 +332,7 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) x[i] = (float)hq[i];
             }
-            const float qs = a.scale_log2;
+            const float qs = EXT ? a.scale : a.scale_log2;      // softcap needs natural units
             qt[rb][ks] = cvt_f16x8(x[0] * qs, x[1] * qs, x[2] * qs, x[3] * qs, x[4] * qs, x[5] * qs,
                                    x[6] * qs, x[7] * qs);
             if constexpr (kAgpr) asm volatile("" : "+a"(qt[rb][ks]));    // its home: AGPRs
@@ -405,8 +408,12 @@ prefill_wide_kernel(PrefillArgs a)
             }
         });
     };
-    // causal / cache-end mask of tile t; wave-uniform test (diagonal and last tiles)
-    auto tile_needs_mask = [&](int t) { return t * BN + BN - 1 > a.q_base + w_first || t * BN + BN > kmax; };
+    // causal / cache-end / window mask of tile t; wave-uniform test (diagonal and last tiles,
+    // and tiles with keys before the window of the wave's last row)
+    auto tile_needs_mask = [&](int t) {
+        return t * BN + BN - 1 > a.q_base + w_first || t * BN + BN > kmax ||
+               (swa && t * BN < a.q_base + w_first + RPW - a.sliding_window);
+    };
     auto mask_tile = [&](STile& sv, int t) {
         const int key0 = t * BN;
 #pragma unroll
@@ -416,7 +423,8 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int key = key0 + 32 * sb + 8 * (v >> 2) + 4 * hh + (v & 3);
-                    const bool vis = key <= qpos[rb] && key < kmax;
+                    bool vis = key <= qpos[rb] && key < kmax;
+                    if (swa) vis = vis && key >= qpos[rb] + 1 - a.sliding_window;
                     sv[rb][sb][v] = vis ? sv[rb][sb][v] : -INFINITY;
                 }
     };
@@ -454,10 +462,18 @@ prefill_wide_kernel(PrefillArgs a)
                 }
 #pragma unroll
                 for (int sb = 0; sb < SB; ++sb) sv[rb][sb] -= d;
+                if constexpr (!EXT)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) negm[rb][v] = -m_used[rb];
+                    for (int v = 0; v < 16; ++v) negm[rb][v] = -m_used[rb];
             }
         }
+    };
+    // EXT: the MFMAs leave raw scaled scores q.k * scale (accumulators seeded with 0); the VALU
+    // softcaps them, converts to log2 units and subtracts the running max
+    const float cap_c1 = EXT && a.softcap > 0.f ? 2.f * kLog2e / a.softcap : 0.f;
+    const float cap_c2 = a.softcap * kLog2e;
+    auto ext_score = [&](float x, int rb) {
+        return (a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e) - m_used[rb];
     };
     // finish tile t's scores: mask if needed, row max, rescale
     auto finish_scores = [&](STile& sv, int t, float (&mx)[NB]) {
@@ -511,7 +527,9 @@ prefill_wide_kernel(PrefillArgs a)
             wait_lgkm<LATER>(ka[i]);
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
-                if constexpr (kAgpr)
+                if constexpr (kAgpr && EXT && ks == 0)
+                    mfma_s_zero(sn[rb][sb], __builtin_bit_cast(f16x8, ka[i]), qt[rb][ks]);   // raw scores
+                else if constexpr (kAgpr)
                     mfma_s<ks == 0>(sn[rb][sb], __builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], negm[rb]);
                 else
                     sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
@@ -585,7 +603,7 @@ prefill_wide_kernel(PrefillArgs a)
         phase_a(std::integral_constant<int, par ^ 1>{}, sc, sn, pw);
         if constexpr (kAgpr) {
             s_settle(sn);                                  // S(tn) is read by the VALU below
-            keep_bias(negm);
+            if constexpr (!EXT) keep_bias(negm);
         }
         __builtin_amdgcn_s_setprio(2);
         // phase B: PV(t) MFMAs, row max of S(tn) on the VALU (running max3 over element pairs)
@@ -602,6 +620,10 @@ prefill_wide_kernel(PrefillArgs a)
                 if constexpr (kSCopy) {
                     sc[rb][sb][v] = sn[rb][sb][v];
                     sc[rb][sb][v + 1] = sn[rb][sb][v + 1];
+                }
+                if constexpr (EXT) {
+                    sx[rb][sb][v] = ext_score(sx[rb][sb][v], rb);
+                    sx[rb][sb][v + 1] = ext_score(sx[rb][sb][v + 1], rb);
                 }
                 mrun[rb] = __builtin_fmaxf(mrun[rb], __builtin_fmaxf(sx[rb][sb][v], sx[rb][sb][v + 1]));
             }
@@ -640,6 +662,13 @@ prefill_wide_kernel(PrefillArgs a)
                 s_tile(sA);
                 if constexpr (kAgpr) s_settle(sA);
             }
+            if constexpr (EXT)
+#pragma unroll
+                for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+                    for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) sA[rb][sb][v] = ext_score(sA[rb][sb][v], rb);
             float mx[NB];
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) mx[rb] = row_max(sA, rb);
@@ -777,42 +806,48 @@ prefill_wide_kernel(PrefillArgs a)
 
 int prefill_wide_rows(int ks) { return (4 / ks) * kWideRowsPerWave; }
 
-template <int HD, int KS, bool QF, bool OF>
+template <int HD, int KS, bool QF, bool OF, bool EXT>
 static hipError_t launch_wide_t(const PrefillArgs& a, hipStream_t stream)
 {
     constexpr int lds_bytes = WideLayout<HD, KS>::LDS_BYTES;
     static bool attr_done = false;        // set once per instantiation (benign race: idempotent)
     if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)prefill_wide_kernel<HD, KS, QF, OF>,
+        hipError_t e = hipFuncSetAttribute((const void*)prefill_wide_kernel<HD, KS, QF, OF, EXT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
         if (e != hipSuccess) return e;
         attr_done = true;
     }
-    hipLaunchKernelGGL((prefill_wide_kernel<HD, KS, QF, OF>), dim3(a.n_items), dim3(kPrefillThreads),
+    hipLaunchKernelGGL((prefill_wide_kernel<HD, KS, QF, OF, EXT>), dim3(a.n_items), dim3(kPrefillThreads),
                        lds_bytes, stream, a);
     return hipGetLastError();
 }
 
-template <int HD, int KS>
-static hipError_t launch_wide_ks(const PrefillArgs& a, bool q_f32, bool o_f32, hipStream_t s)
+template <int HD, int KS, bool EXT>
+static hipError_t launch_wide_qo(const PrefillArgs& a, bool q_f32, bool o_f32, hipStream_t s)
 {
-    if (q_f32) return o_f32 ? launch_wide_t<HD, KS, true, true>(a, s) : launch_wide_t<HD, KS, true, false>(a, s);
-    return o_f32 ? launch_wide_t<HD, KS, false, true>(a, s) : launch_wide_t<HD, KS, false, false>(a, s);
+    if (q_f32) return o_f32 ? launch_wide_t<HD, KS, true, true, EXT>(a, s) : launch_wide_t<HD, KS, true, false, EXT>(a, s);
+    return o_f32 ? launch_wide_t<HD, KS, false, true, EXT>(a, s) : launch_wide_t<HD, KS, false, false, EXT>(a, s);
+}
+
+template <int HD, int KS>
+static hipError_t launch_wide_ks(const PrefillArgs& a, bool q_f32, bool o_f32, bool ext, hipStream_t s)
+{
+    return ext ? launch_wide_qo<HD, KS, true>(a, q_f32, o_f32, s) : launch_wide_qo<HD, KS, false>(a, q_f32, o_f32, s);
 }
 
 bool prefill_wide_supported(int head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 
-hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32,
+hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32, bool ext,
                                hipStream_t stream)
 {
     if (ks != 1 && ks != 2) return hipErrorInvalidValue;
     switch (head_dim) {
-    case 64: return ks == 1 ? launch_wide_ks<64, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<64, 2>(a, q_f32, o_f32, stream);
-    case 128: return ks == 1 ? launch_wide_ks<128, 1>(a, q_f32, o_f32, stream) : launch_wide_ks<128, 2>(a, q_f32, o_f32, stream);
+    case 64: return ks == 1 ? launch_wide_ks<64, 1>(a, q_f32, o_f32, ext, stream) : launch_wide_ks<64, 2>(a, q_f32, o_f32, ext, stream);
+    case 128: return ks == 1 ? launch_wide_ks<128, 1>(a, q_f32, o_f32, ext, stream) : launch_wide_ks<128, 2>(a, q_f32, o_f32, ext, stream);
     // head dim 256: 128-row blocks only.  Two key groups per workgroup need more registers
     // than one wave per SIMD has (the merge and the second group's state); the compiler then
     // moves accumulator blocks between register files right beside the inline-asm MFMAs.
-    case 256: return ks == 1 ? launch_wide_ks<256, 1>(a, q_f32, o_f32, stream) : hipErrorInvalidValue;
+    case 256: return ks == 1 ? launch_wide_ks<256, 1>(a, q_f32, o_f32, ext, stream) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }

@@ -90,6 +90,13 @@ PREFILL_CASES = [
     (4, 4, 64, 100, 3000, 0, False, False, 0, 0.0),    # 12 splits: a partial second merge batch
     (8, 1, 256, 64, 4000, 0, True, True, 0, 0.0),      # 16 splits: two full merge batches
     (6, 2, 192, 70, 2000, 0, True, False, 0, 0.0),
+    # pipelined kernel with softcap / sliding window (raw MFMA scores, VALU softcap; window
+    # tiles skipped below the block's first row, masked above)
+    (16, 4, 128, 520, 100, 0, True, True, 300, 0.0),     # window, 64-row blocks, ragged
+    (64, 8, 128, 512, 2000, 0, False, False, 200, 20.0), # window + softcap, 128-row blocks, f32 q/o
+    (16, 2, 256, 300, 1000, 0, True, True, 0, 50.0),     # hd 256 softcap in key splits
+    (8, 2, 64, 200, 5000, 0, True, False, 1000, 0.0),    # hd 64 window in key splits
+    (8, 2, 256, 256, 0, 0, False, True, 100, 30.0),      # hd 256 window + softcap, cold
 ]
 
 
@@ -122,8 +129,8 @@ def test_prefill_golden(hip, golden):
 
 @pytest.mark.parametrize("cap", [0.0, 30.0])
 def test_prefill_split_equals_unsplit(hip, cap):
-    """With a workspace the kernel may split the key range (the softcap shape takes the split
-    path of prefill_kernel); the result must not depend on it."""
+    """With a workspace the pipelined kernel splits this short chunk's key range over
+    workgroups (plain and softcapped); the result must not depend on it."""
     hq, hkv, hd, nq, base = 8, 2, 128, 256, 3000
     q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=base + nq, seed=4, q_f16=True)
     a = run_prefill(q, k, v, hkv=hkv, n_ctx=base + nq, q_base=base, q_f16=True, cap=cap, split=True)
