@@ -97,6 +97,10 @@ PREFILL_CASES = [
     (16, 2, 256, 300, 1000, 0, True, True, 0, 50.0),     # hd 256 softcap in key splits
     (8, 2, 64, 200, 5000, 0, True, False, 1000, 0.0),    # hd 64 window in key splits
     (8, 2, 256, 256, 0, 0, False, True, 100, 30.0),      # hd 256 window + softcap, cold
+    # 64-row blocks at one to one and a half per CU (cfg2's regime)
+    (32, 8, 128, 512, 100, 0, True, True, 0, 0.0),       # exactly one block per CU
+    (40, 8, 128, 520, 300, 0, False, False, 0, 0.0),     # 360 blocks, ragged last block
+    (36, 4, 64, 512, 700, 0, True, False, 200, 10.0),    # hd 64, window + softcap
 ]
 
 
@@ -156,6 +160,7 @@ GATED_PREFILL_CASES = [
     (6, 2, 192, 70, 10, True, True, 0, 0.0, True),         # general kernel, hd 192
     (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # general kernel, softcap
     (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # general kernel's key split + combine
+    (40, 8, 128, 520, 300, True, True, 0, 0.0, True),      # pipelined kernel, 360 64-row blocks
 ]
 
 
