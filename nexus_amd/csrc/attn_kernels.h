@@ -108,6 +108,7 @@ inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
 }
 
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.
+// prefill_kernel (attn_prefill.hip): head dim 192 (hipErrorInvalidValue for others).
 hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                           hipStream_t stream);
 // Wide (pipelined) prefill: causal shapes at the head dims prefill_wide_supported() accepts,

@@ -4,7 +4,8 @@
 // attn_flash.comp (src/gpu/shaders/attn_flash.comp:66-72, 121-159): query i sits at
 // absolute position q_base + i and sees keys [start, min(q_base + i, n_ctx - 1)].
 //
-// Design (one workgroup = 128 queries of one q head, 4 waves x 32 queries, 2 per CU):
+// Built for head dim 192 (the pipelined kernel in attn_prefill_wide.hip covers 64, 128 and
+// 256).  Design (one workgroup = 128 queries of one q head, 4 waves x 32 queries, 2 per CU):
 //  * K/V tiles (BN keys) go from HBM straight into LDS with buffer-load-to-LDS (16 bytes
 //    per lane, no VGPR staging, no transpose work) through a ring of STAGES buffers: the
 //    next STAGES - 1 tiles are in flight while the current one is consumed, one barrier
@@ -459,11 +460,9 @@ static hipError_t launch_prefill_hd(const PrefillArgs& a, bool q_f32, bool o_f32
 hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                           hipStream_t stream)
 {
+    // head dims 64, 128 and 256 run on the pipelined kernel (attn_prefill_wide.hip)
     switch (head_dim) {
-    case 64: return launch_prefill_hd<64>(a, q_f32, o_f32, ext, stream);
-    case 128: return launch_prefill_hd<128>(a, q_f32, o_f32, ext, stream);
     case 192: return launch_prefill_hd<192>(a, q_f32, o_f32, ext, stream);
-    case 256: return launch_prefill_hd<256>(a, q_f32, o_f32, ext, stream);
     default: return hipErrorInvalidValue;
     }
 }
