@@ -4,12 +4,14 @@
 // Semantics are those of prefill_kernel (attn_prefill.hip), i.e. Transformer::attn_batch_cpu
 // (src/model/transformer.h:8653-8685) and attn_flash.comp (src/gpu/shaders/attn_flash.comp:
 // 66-72, 121-159): query i sits at absolute position q_base + i and sees keys
-// [0, min(q_base + i, n_ctx - 1)].  This kernel takes the plain causal shapes (no logit
-// softcap, no sliding window); prefill_kernel keeps those.  A key split across workgroups
-// writes the reference's split-K partials for the combine kernel, as prefill_kernel does.
+// [start, min(q_base + i, n_ctx - 1)], start = q_base + i + 1 - window with a sliding window,
+// scores softcapped when softcap > 0 (the EXT instantiation).  Head dims 64, 128 and 256;
+// prefill_kernel serves 192.  A key split across workgroups writes the reference's split-K
+// partials for the combine kernel.
 //
 // Design:
-//  * A wave owns 32 query rows; two waves per SIMD.  Workgroup = 4 waves.  KS = 1: four row
+//  * A wave owns 32 query rows; two waves per SIMD (one at head dim 256, with O and Q^T in
+//    AGPRs and the MFMAs as inline asm).  Workgroup = 4 waves.  KS = 1: four row
 //    waves (128 query rows) share every K/V tile.  KS = 2: two row waves x two key groups
 //    (64 rows); key group g takes the tiles t = g (mod 2) and the groups' (O, m, l) merge
 //    through LDS at the end -- for short chunks, where 128-row blocks leave CUs idle.
@@ -27,7 +29,9 @@
 //    the slot parity is static, so every LDS address is a per-lane register plus an immediate.
 //  * S^T = K Q^T with Q pre-scaled by scale * log2(e) and the accumulator seeded with -m, so a
 //    probability is one exp2; the running max moves lazily (only past a 2^8 margin), the row
-//    max is v_max3 + v_permlane32_swap, row sums are fp32 adds of the probabilities.
+//    max is v_max3 + v_permlane32_swap, row sums are fp32 adds of the probabilities.  EXT:
+//    Q pre-scaled by scale, accumulators seeded with 0, and the VALU turns each raw score into
+//    softcap * tanh(x / softcap) * log2(e) - m (or x * log2(e) - m) before the row max.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
