@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 namespace nxa {
@@ -184,6 +185,22 @@ __device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, uint32_t b
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t byte_off)
 {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+
+// Host side: raise a kernel's dynamic LDS limit (hipFuncAttributeMaxDynamicSharedMemorySize)
+// once per device.  The attribute belongs to the device current at the call, so a process
+// that drives several GPUs sets it on each; `done` is the kernel's bitmask of devices already
+// set (device ids below 64; others set it on every launch).
+inline hipError_t ensure_dyn_lds(const void* kernel, int bytes, std::atomic<uint64_t>& done)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit && (done.load(std::memory_order_relaxed) & bit)) return hipSuccess;
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_relaxed);
+    return e;
 }
 
 }  // namespace nxa

@@ -576,13 +576,9 @@ template <int HD, int RT, bool QF, bool OF, bool EXT>
 static hipError_t launch_decode_t(const DecodeArgs& a, int n_rowgroups, hipStream_t stream)
 {
     constexpr int lds_bytes = DecodeLayout<HD, RT>::LDS_BYTES;
-    static bool attr_done = false;        // set once per instantiation (idempotent)
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)decode_part_kernel<HD, RT, QF, OF, EXT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};          // devices whose LDS limit is raised
+    const hipError_t e = ensure_dyn_lds((const void*)decode_part_kernel<HD, RT, QF, OF, EXT>, lds_bytes, lds_set);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((decode_part_kernel<HD, RT, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
                        dim3(64 * DecodeLayout<HD, RT>::NW), lds_bytes, stream, a);
     return hipGetLastError();

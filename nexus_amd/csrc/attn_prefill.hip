@@ -434,13 +434,9 @@ template <int HD, bool QF, bool OF, bool EXT>
 static hipError_t launch_prefill_t(const PrefillArgs& a, hipStream_t stream)
 {
     constexpr int lds_bytes = PrefillLayout<HD>::LDS_BYTES;
-    static bool attr_done = false;        // set once per instantiation (benign race: idempotent)
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<HD, QF, OF, EXT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};          // devices whose LDS limit is raised
+    const hipError_t e = ensure_dyn_lds((const void*)prefill_kernel<HD, QF, OF, EXT>, lds_bytes, lds_set);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((prefill_kernel<HD, QF, OF, EXT>), dim3(a.n_items), dim3(kPrefillThreads),
                        lds_bytes, stream, a);
     return hipGetLastError();

@@ -814,13 +814,9 @@ template <int HD, int KS, bool QF, bool OF, bool EXT>
 static hipError_t launch_wide_t(const PrefillArgs& a, hipStream_t stream)
 {
     constexpr int lds_bytes = WideLayout<HD, KS>::LDS_BYTES;
-    static bool attr_done = false;        // set once per instantiation (benign race: idempotent)
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void*)prefill_wide_kernel<HD, KS, QF, OF, EXT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};          // devices whose LDS limit is raised
+    const hipError_t e = ensure_dyn_lds((const void*)prefill_wide_kernel<HD, KS, QF, OF, EXT>, lds_bytes, lds_set);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((prefill_wide_kernel<HD, KS, QF, OF, EXT>), dim3(a.n_items), dim3(kPrefillThreads),
                        lds_bytes, stream, a);
     return hipGetLastError();
