@@ -202,14 +202,12 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
     return s < 1 ? 1 : (int)s;
 }
 
-// Prefill kernel choice.  Shapes at the head dims the pipelined kernel covers (64, 128, 256;
-// softcap and sliding window included) take it: 128-row blocks (KS = 1), or 64-row blocks with
-// the key range split over two waves of the workgroup (KS = 2) when 128-row blocks leave
-// CUs without a workgroup (head dim 256 has the 128-row form only: the two-key-group form
-// does not fit one wave per SIMD's registers).  Either grid splits the key range over
-// workgroups by the rule above.  Head dim 192 takes prefill_kernel with the same rule.
+// Prefill grid of the pipelined kernel (every supported head dim, softcap and sliding window
+// included): 128-row blocks (KS = 1), or 64-row blocks with the key range split over two waves
+// of the workgroup (KS = 2) when 128-row blocks leave CUs without a workgroup (head dims 192
+// and 256 have the 128-row form only: the two-key-group form does not fit one wave per SIMD's
+// registers).  Either grid splits the key range over workgroups by the rule above.
 struct PrefillPlan {
-    bool wide;
     int ks;
     int splits;
 };
@@ -221,15 +219,10 @@ long long query_blocks(const nexus_attn_desc* d, long long rows)
 
 PrefillPlan prefill_plan(const nexus_attn_desc* d)
 {
-    PrefillPlan p{false, 1, 1};
-    if (nxa::prefill_wide_supported(d->head_dim)) {
-        const bool few = query_blocks(d, nxa::prefill_wide_rows(1)) < device_cus();
-        p.wide = true;
-        p.ks = few && d->head_dim != 256 ? 2 : 1;
-        p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks)));
-        return p;
-    }
-    p.splits = prefill_splits(d, query_blocks(d, nxa::kPrefillBM));
+    PrefillPlan p{1, 1};
+    const bool few = query_blocks(d, nxa::prefill_wide_rows(1)) < device_cus();
+    p.ks = few && d->head_dim <= 128 ? 2 : 1;
+    p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks)));
     return p;
 }
 
@@ -440,15 +433,14 @@ int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, con
     a.scale = eff_scale(desc);
     a.scale_log2 = a.scale * 1.4426950408889634f;
     a.softcap = desc->softcap;
-    const long long rows = plan.wide ? nxa::prefill_wide_rows(plan.ks) : nxa::kPrefillBM;
+    const long long rows = nxa::prefill_wide_rows(plan.ks);
     a.n_qblocks = (int)((desc->n_query + rows - 1) / rows);
     a.n_splits = splits;
     const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
     if (items > INT_MAX) return capi_fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
     const bool q32 = desc->q_dtype == NEXUS_DT_F32, o32 = desc->o_dtype == NEXUS_DT_F32;
-    hipError_t e = plan.wide ? nxa::launch_prefill_wide(a, desc->head_dim, plan.ks, q32, o32, is_ext(desc), s)
-                             : nxa::launch_prefill(a, desc->head_dim, q32, o32, is_ext(desc), s);
+    const hipError_t e = nxa::launch_prefill_wide(a, desc->head_dim, plan.ks, q32, o32, is_ext(desc), s);
     if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
     if (splits > 1) {
         const int rc2 = launch_combine_for(desc, (float*)workspace, out, gate, splits, s);

@@ -7,9 +7,7 @@
 
 namespace nxa {
 
-// Prefill: 128 queries x one q head per workgroup (4 waves x 32 rows); the key tile per
-// head dim is set with the kernel (attn_prefill.hip).
-constexpr int kPrefillBM = 128;
+// Prefill workgroup size (attn_prefill_wide.hip): 4 waves.
 constexpr int kPrefillThreads = 256;
 // Pipelined prefill (attn_prefill_wide.hip): 32 query rows per wave, 4 waves per workgroup
 // as 4 row waves (KS = 1, 128 rows) or 2 row waves x 2 key groups (KS = 2, 64 rows).
@@ -108,12 +106,8 @@ inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
 }
 
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.
-// prefill_kernel (attn_prefill.hip): head dim 192 (hipErrorInvalidValue for others).
-hipError_t launch_prefill(const PrefillArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
-                          hipStream_t stream);
-// Wide (pipelined) prefill: causal shapes at the head dims prefill_wide_supported() accepts,
+// Pipelined prefill: causal shapes at head dims 64, 128, 192, 256 (KS = 2 at 64 and 128 only),
 // with softcap and sliding window when `ext`; n_qblocks counts prefill_wide_rows(ks)-row blocks.
-bool prefill_wide_supported(int head_dim);
 int prefill_wide_rows(int ks);
 hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32, bool ext,
                                hipStream_t stream);

@@ -1,17 +1,16 @@
 // nexus_amd/csrc/attn_prefill_wide.hip -- software-pipelined causal GQA flash-attention
 // prefill for gfx950.
 //
-// Semantics are those of prefill_kernel (attn_prefill.hip), i.e. Transformer::attn_batch_cpu
-// (src/model/transformer.h:8653-8685) and attn_flash.comp (src/gpu/shaders/attn_flash.comp:
-// 66-72, 121-159): query i sits at absolute position q_base + i and sees keys
-// [start, min(q_base + i, n_ctx - 1)], start = q_base + i + 1 - window with a sliding window,
-// scores softcapped when softcap > 0 (the EXT instantiation).  Head dims 64, 128 and 256;
-// prefill_kernel serves 192.  A key split across workgroups writes the reference's split-K
-// partials for the combine kernel.
+// Semantics are those of Transformer::attn_batch_cpu (src/model/transformer.h:8653-8685) and
+// attn_flash.comp (src/gpu/shaders/attn_flash.comp:66-72, 121-159): query i sits at absolute
+// position q_base + i and sees keys [start, min(q_base + i, n_ctx - 1)], start = q_base + i +
+// 1 - window with a sliding window, scores softcapped when softcap > 0 (the EXT
+// instantiation).  Head dims 64, 128, 192 and 256.  A key split across workgroups writes the
+// reference's split-K partials for the combine kernel.
 //
 // Design:
-//  * A wave owns 32 query rows; two waves per SIMD (one at head dim 256, with O and Q^T in
-//    AGPRs and the MFMAs as inline asm).  Workgroup = 4 waves.  KS = 1: four row
+//  * A wave owns 32 query rows; two waves per SIMD (one at head dims 192 and 256, with O and
+//    Q^T in AGPRs and the MFMAs as inline asm).  Workgroup = 4 waves.  KS = 1: four row
 //    waves (128 query rows) share every K/V tile.  KS = 2: two row waves x two key groups
 //    (64 rows); key group g takes the tiles t = g (mod 2) and the groups' (O, m, l) merge
 //    through LDS at the end -- for short chunks, where 128-row blocks leave CUs idle.
@@ -25,7 +24,7 @@
 //    O, Q^T and both S^T tiles keep fixed registers (the last step is peeled).
 //  * K runs one tile ahead of V in an LDS ring of two tiles per operand: step s reads K(s+1)
 //    and V(s) while K(s+2) and V(s+1) load (buffer-load-to-LDS of XOR-swizzled 16-byte chunks,
-//    the slot layout of prefill_kernel); one barrier per step.  With the loop unrolled by two
+//    each lane choosing the global chunk for its LDS slot); one barrier per step.  With the loop unrolled by two
 //    the slot parity is static, so every LDS address is a per-lane register plus an immediate.
 //  * S^T = K Q^T with Q pre-scaled by scale * log2(e) and the accumulator seeded with -m, so a
 //    probability is one exp2; the running max moves lazily (only past a 2^8 margin), the row
@@ -70,9 +69,9 @@ struct WideLayout {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
-// Slot of global chunk c of K row r and of V row r (the conflict-free layouts of
-// prefill_kernel: a K operand read spreads its 32 rows over 16 slots; a transposing V read
-// puts its 4 rows x 64 bytes per 32 lanes on disjoint banks).
+// Slot of global chunk c of K row r and of V row r (XOR swizzles that keep the operand reads
+// free of bank conflicts: a K operand read spreads its 32 rows over 16 slots; a transposing V
+// read puts its 4 rows x 64 bytes per 32 lanes on disjoint banks).
 template <int HD>
 __device__ __forceinline__ int wk_slot(int r, int c) { return c ^ (r & WideLayout<HD, 1>::SWZ); }
 template <int HD>
@@ -249,16 +248,27 @@ prefill_wide_kernel(PrefillArgs a)
     // The K swizzle depends on the row modulo 16 and the V swizzle on the row modulo 4 (or
     // 2), and load j + 1 lands 4096 bytes after load j: 16 or more rows at head dim <= 128,
     // so one per-lane offset serves every load (load j adds 4096 j); 8 rows at head dim 256,
-    // where loads of odd j take the K offset of the row 8 further on.
-    constexpr int RPL = kPrefillThreads * 16 / L::ROW;    // rows per load
-    static_assert(RPL % 16 == 0 || RPL == 8, "swizzle period");
-    uint32_t koff[2], voff;
-    {
+    // where loads of odd j take the K offset of the row 8 further on.  At head dim 192 (rows
+    // of 384 bytes) a load covers 10 2/3 rows: each load has its own offsets.
+    constexpr bool kRowAligned = 4096 % L::ROW == 0;
+    constexpr int RPL = kRowAligned ? kPrefillThreads * 16 / L::ROW : 0;   // rows per load
+    static_assert(!kRowAligned || RPL % 16 == 0 || RPL == 8, "swizzle period");
+    constexpr int NKOFF = kRowAligned ? 2 : L::LOADS, NVOFF = kRowAligned ? 1 : L::LOADS;
+    int koff[NKOFF], voff[NVOFF];                          // minus 4096 j, added back per load
+    if constexpr (kRowAligned) {
         const int b = 16 * tid;
         const int row = b / L::ROW, slot = (b % L::ROW) / 16;
-        koff[0] = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row, slot));
-        koff[1] = (uint32_t)(row * L::ROW + 16 * wk_slot<HD>(row + RPL, slot));
-        voff = (uint32_t)(row * L::ROW + 16 * wv_slot<HD>(row, slot));
+        koff[0] = row * L::ROW + 16 * wk_slot<HD>(row, slot);
+        koff[1] = row * L::ROW + 16 * wk_slot<HD>(row + RPL, slot);
+        voff[0] = row * L::ROW + 16 * wv_slot<HD>(row, slot);
+    } else {
+#pragma unroll
+        for (int j = 0; j < L::LOADS; ++j) {
+            const int b = 16 * tid + 4096 * j;
+            const int row = b / L::ROW, slot = (b % L::ROW) / 16;
+            koff[j] = row * L::ROW + 16 * wk_slot<HD>(row, slot) - 4096 * j;
+            voff[j] = row * L::ROW + 16 * wv_slot<HD>(row, slot) - 4096 * j;
+        }
     }
     // tiles of step `st`: tile st * KS + i goes to slot (st % 2) * KS + i.  Loads past the cache
     // end are issued too (the descriptor returns zeros): every step issues the same number of
@@ -273,12 +283,15 @@ prefill_wide_kernel(PrefillArgs a)
             const int base = (t0 + st * KS + i) * BN * L::ROW;
             lds_u8* dst = lds3 + (k_side ? 0 : L::VBASE) + (slot0 + i) * L::TILE + 1024 * wave;
 #pragma unroll
-            for (int j = 0; j < L::LOADS; ++j)
+            for (int j = 0; j < L::LOADS; ++j) {
                 // the whole offset in the vector operand: the descriptor's range check
-                // (zeros past the cache end) covers it
+                // (zeros past the cache end) covers it.  (Computed before the builtin: with the
+                // array selection inside its argument list the host pass drops the kernel.)
+                const int goff = (k_side ? koff[kRowAligned ? (RPL == 8 ? (j & 1) : 0) : j]
+                                         : voff[kRowAligned ? 0 : j]) + base + 4096 * j;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    k_side ? krs : vrs, (void __attribute__((address_space(3)))*)(dst + 4096 * j), 16,
-                    (int)(k_side ? koff[RPL == 8 ? (j & 1) : 0] : voff) + base + 4096 * j, 0, 0, 0);
+                    k_side ? krs : vrs, (void __attribute__((address_space(3)))*)(dst + 4096 * j), 16, goff, 0, 0, 0);
+            }
         }
     };
     // group st: what step st consumes, K(st + 1) and V(st)
@@ -835,8 +848,6 @@ static hipError_t launch_wide_ks(const PrefillArgs& a, bool q_f32, bool o_f32, b
     return ext ? launch_wide_qo<HD, KS, true>(a, q_f32, o_f32, s) : launch_wide_qo<HD, KS, false>(a, q_f32, o_f32, s);
 }
 
-bool prefill_wide_supported(int head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
-
 hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32, bool ext,
                                hipStream_t stream)
 {
@@ -847,6 +858,7 @@ hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool 
     // head dim 256: 128-row blocks only.  Two key groups per workgroup need more registers
     // than one wave per SIMD has (the merge and the second group's state); the compiler then
     // moves accumulator blocks between register files right beside the inline-asm MFMAs.
+    case 192: return ks == 1 ? launch_wide_ks<192, 1>(a, q_f32, o_f32, ext, stream) : hipErrorInvalidValue;
     case 256: return ks == 1 ? launch_wide_ks<256, 1>(a, q_f32, o_f32, ext, stream) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }

@@ -30,6 +30,22 @@ def test_library_exports_every_declared_symbol():
     assert "gfx950" in capi.version()
 
 
+def test_library_has_no_undefined_kernel_symbols():
+    """Every kernel the library launches is defined in it.  (hipcc's host pass can drop a kernel
+    template without a diagnostic -- seen when a buffer-load-to-LDS builtin's argument list held an
+    array selection -- and the library then references the missing stub.)"""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("no nm on this host")
+    res = subprocess.run([nm, "-D", "--undefined-only", str(capi.LIB_PATH)], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    missing = [line.split()[-1] for line in res.stdout.splitlines() if "nxa" in line]
+    assert not missing, missing[:8]
+
+
 @pytest.mark.parametrize("cls,cname", [(capi.AttnDesc, "nexus_attn_desc"), (capi.PrepDesc, "nexus_attn_prep_desc"),
                                        (capi.KvLayerView, "nexus_kv_layer_view")])
 def test_desc_layout_matches_header(tmp_path, cls, cname):

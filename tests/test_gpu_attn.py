@@ -86,7 +86,7 @@ PREFILL_CASES = [
     # head dim 256 with fewer blocks than CUs: 128-row blocks, unsplit or in key splits
     (16, 2, 256, 1030, 0, 0, True, True, 0, 0.0),
     (16, 4, 256, 64, 500, 0, True, False, 0, 0.0),
-    # key splits merged by the one-wave-per-row combine (>= 256 rows); hd 192 on prefill_kernel
+    # key splits merged by the one-wave-per-row combine (>= 256 rows); hd 192 in AGPRs
     (4, 4, 64, 100, 3000, 0, False, False, 0, 0.0),    # 12 splits: a partial second merge batch
     (8, 1, 256, 64, 4000, 0, True, True, 0, 0.0),      # 16 splits: two full merge batches
     (6, 2, 192, 70, 2000, 0, True, False, 0, 0.0),
