@@ -131,6 +131,23 @@ def test_prefill_golden(hip, golden):
     assert_close(got, golden["pre_a_out"], "golden pre_a")
 
 
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,sw,cap", [
+    (8, 2, 128, 1, 500, 0, 0.0),        # one row of a 64-row block
+    (16, 2, 256, 3, 900, 0, 0.0),       # AGPR form, three rows
+    (12, 4, 192, 5, 300, 64, 25.0),     # head dim 192, window + softcap
+    (4, 4, 64, 2, 0, 0, 0.0),           # cold, two queries
+])
+def test_prefill_tiny_chunks_without_workspace(hip, hq, hkv, hd, nq, base, sw, cap):
+    """A handful of queries and no workspace: the pipelined kernel runs blocks that are almost
+    all padding rows (the split-KV path needs the workspace)."""
+    n_ctx = base + nq
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=nq + hd, q_f16=True)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, q_f16=True, sw=sw, cap=cap, split=False)
+    ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, sliding_window=sw, softcap=cap,
+                       n_threads=8)
+    assert_close(got, ref, f"tiny {hq}/{hkv} hd{hd} nq{nq}@{base}")
+
+
 @pytest.mark.parametrize("cap", [0.0, 30.0])
 def test_prefill_split_equals_unsplit(hip, cap):
     """With a workspace the pipelined kernel splits this short chunk's key range over
