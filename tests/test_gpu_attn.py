@@ -174,9 +174,11 @@ GATED_PREFILL_CASES = [
     (8, 2, 128, 80, 0, True, True, 0, 0.0, True),          # pipelined kernel, 64-row blocks (key-group merge)
     (16, 2, 256, 96, 40, True, True, 0, 0.0, True),        # pipelined kernel, hd 256
     (8, 2, 128, 64, 2000, True, False, 0, 0.0, True),      # pipelined kernel's key split + row combine
-    (6, 2, 192, 70, 10, True, True, 0, 0.0, True),         # general kernel, hd 192
-    (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # general kernel, softcap
-    (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # general kernel's key split + combine
+    (6, 2, 192, 70, 10, True, True, 0, 0.0, True),         # pipelined kernel, hd 192 (AGPR form)
+    (8, 1, 256, 64, 4000, True, False, 0, 0.0, True),      # hd 256 in 16 key splits: gate in the row combine
+    (6, 2, 192, 70, 2000, False, True, 300, 20.0, True),   # hd 192 key splits, window + softcap
+    (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # pipelined kernel, softcap
+    (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # softcapped key split + combine
     (40, 8, 128, 520, 300, True, True, 0, 0.0, True),      # pipelined kernel, 360 64-row blocks
 ]
 
