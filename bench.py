@@ -42,6 +42,10 @@ CONFIGS = {
                  desc="decode 1 token, 40q/8kv, hd128, 61440 keys, 64 splits, f32 LSE combine"),
     "q35p": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=8192, base=0, n_ctx=8192, q="f16", o="f16",
                  desc="cold prefill 8192 tokens, 16q/2kv, hd256 (the Qwen3.5 full-attention layer's shape)"),
+    "cap2": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=512, base=4096, n_ctx=4608, q="f16", o="f16", cap=30.0,
+                 desc="cfg2's shape with logit softcap 30 (Gemma-style), f16 Q/K/V/O"),
+    "swa3": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=8192, base=0, n_ctx=8192, q="f16", o="f16", sw=4096,
+                 desc="cfg3's shape with a 4096-token sliding window (work counted over visible pairs)"),
     "q35c": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=512, base=32768, n_ctx=33280, q="f16", o="f16",
                  desc="chunked prefill 512 queries after 32768 cached tokens, 16q/2kv, hd256 (key splits + combine)"),
     "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
@@ -57,7 +61,7 @@ def work_of(c: dict) -> tuple[float, str]:
     from nexus_amd import capi
 
     if c["kind"] == "prefill":
-        return capi.prefill_flops(c["hq"], c["hd"], c["nq"], c["base"], c["n_ctx"]), "flop"
+        return capi.prefill_flops(c["hq"], c["hd"], c["nq"], c["base"], c["n_ctx"], c.get("sw", 0)), "flop"
     n_keys = min(c["base"] + c["nq"] - 1, c["n_ctx"] - 1) + 1
     return capi.decode_bytes(c["hkv"], c["hd"], n_keys, c["hq"], c["nq"]), "byte"
 
@@ -100,7 +104,8 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False, rotate: boo
         kvs.append((k, v))
     out = torch.empty(c["nq"], c["hq"], c["hd"], dtype=odt, device=dev)
     desc = capi.make_desc(n_q_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"], n_query=c["nq"],
-                          q_base_pos=c["base"], n_ctx=c["n_ctx"],
+                          q_base_pos=c["base"], n_ctx=c["n_ctx"], softcap=c.get("cap", 0.0),
+                          sliding_window=c.get("sw", 0),
                           q_dtype=capi.NEXUS_DT_F16 if qdt == torch.float16 else capi.NEXUS_DT_F32,
                           o_dtype=capi.NEXUS_DT_F16 if odt == torch.float16 else capi.NEXUS_DT_F32)
     if c["kind"] == "decode":
@@ -372,6 +377,8 @@ def main() -> int:
     extra["cfg5_warm"] = measure("cfg5", args.steps, args.warmup, rotate=False)
     extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup)
     extra["q35c"] = measure("q35c", args.steps, args.warmup)
+    extra["cap2"] = measure("cap2", args.steps, args.warmup)
+    extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
 
     cpu = None
