@@ -58,7 +58,11 @@ struct DecodeLayout {
     static constexpr int Q_BYTES = RT * KS * 2 * 64 * 16;     // Q^T operands (hi, lo) per workgroup
     static constexpr int OREGS = RT * DT * 4;                 // f32 O^T values per lane
     static constexpr int MERGE_SLOT = (OREGS + 2 * RT) * 64 * 4;
-    static constexpr int MAIN_BYTES = (NW * VT_WAVE > (NW / 2) * MERGE_SLOT) ? NW * VT_WAVE : (NW / 2) * MERGE_SLOT;
+    // merge: a tree through NW / 2 slots at four waves; at eight, every wave's slot at once
+    // (one barrier, then each wave folds all eight for its share of the dims)
+    static constexpr bool FLAT_MERGE = NW == 8;
+    static constexpr int MERGE_BYTES = (FLAT_MERGE ? NW : NW / 2) * MERGE_SLOT;
+    static constexpr int MAIN_BYTES = NW * VT_WAVE > MERGE_BYTES ? NW * VT_WAVE : MERGE_BYTES;
     static constexpr int LDS_BYTES = MAIN_BYTES + Q_BYTES;
     static_assert(VB >= 1 && (KEYS / 4) * (HD / 8) % 64 == 0, "V staging");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
@@ -355,16 +359,56 @@ decode_part_kernel(DecodeArgs a)
             m[rt] = M;
         }
     };
-#pragma unroll
-    for (int half = NW / 2; half >= 1; half /= 2) {
-        if (wave >= half && wave < 2 * half) put((float*)(lds + (wave - half) * L::MERGE_SLOT));
+    if constexpr (L::FLAT_MERGE) {
+        // every wave hands its (O, m, l) over at once; wave w then folds the eight slots for
+        // the dim tiles dt = w, w + NW, ... (into o[rt][dt], with lt and m the merged row
+        // values) and writes those dims
+        put((float*)(lds + wave * L::MERGE_SLOT));
         __syncthreads();
-        if (wave < half) take((const float*)(lds + wave * L::MERGE_SLOT));
-        if (half > 1) __syncthreads();                     // slots are rewritten next level
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float ms[NW], M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                ms[w] = ((const float*)(lds + w * L::MERGE_SLOT))[(L::OREGS + 2 * rt) * 64 + lane];
+                M = fmaxf(M, ms[w]);
+            }
+            float Lt = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float* sl = (const float*)(lds + w * L::MERGE_SLOT);
+                ms[w] = fast_exp2(ms[w] - M);                // the slot's weight
+                Lt += sl[(L::OREGS + 2 * rt + 1) * 64 + lane] * ms[w];
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                if (dt % NW != wave) continue;               // wave-uniform
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    const float* sl = (const float*)(lds + w * L::MERGE_SLOT);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i] += sl[((rt * DT + dt) * 4 + i) * 64 + lane] * ms[w];
+                }
+                o[rt][dt] = acc;
+            }
+            lt[rt] = Lt;
+            m[rt] = M;
+        }
+    } else {
+#pragma unroll
+        for (int half = NW / 2; half >= 1; half /= 2) {
+            if (wave >= half && wave < 2 * half) put((float*)(lds + (wave - half) * L::MERGE_SLOT));
+            __syncthreads();
+            if (wave < half) take((const float*)(lds + wave * L::MERGE_SLOT));
+            if (half > 1) __syncthreads();                 // slots are rewritten next level
+        }
+        if (wave != 0) return;
     }
-    if (wave != 0) return;
+    // dim tiles this wave writes: all (tree merge: wave 0), or dt = wave, wave + NW, ... (flat)
+    auto mine = [&](int dt) { return !L::FLAT_MERGE || dt % NW == wave; };
 
-    // ---- wave 0: lane (row n, group g) holds dims 16*dt + 4*g + (0..3) of its rows
+    // ---- lane (row n, group g) holds dims 16*dt + 4*g + (0..3) of its rows
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         if (!rok[rt]) continue;
@@ -373,6 +417,7 @@ decode_part_kernel(DecodeArgs a)
             const float inv = lt[rt] > 0.f ? 1.f / lt[rt] : 0.f;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
+                if (!mine(dt)) continue;
                 const int dim = 16 * dt + 4 * g;
                 const f32x4 y = o[rt][dt] * inv * gate4(a.gate, prow * HD + dim);
                 if constexpr (O_F32) {
@@ -389,11 +434,12 @@ decode_part_kernel(DecodeArgs a)
             float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
+                if (!mine(dt)) continue;
                 const int dim = 16 * dt + 4 * g;
                 *(f32x2*)(pr + dim) = f32x2{o[rt][dt][0], o[rt][dt][1]};
                 *(f32x2*)(pr + dim + 2) = f32x2{o[rt][dt][2], o[rt][dt][3]};
             }
-            if (g == 0) *(f32x2*)(pr + HD) = f32x2{m[rt] * kLn2, lt[rt]};   // m in natural-log units
+            if (g == 0 && wave == 0) *(f32x2*)(pr + HD) = f32x2{m[rt] * kLn2, lt[rt]};   // m in natural-log units
         }
     }
 }
