@@ -33,7 +33,9 @@
 //    in flight per wave (one step from hd x rows > 128, with two waves per SIMD).  The Q^T
 //    operands (f16 high/low parts) sit in LDS, one copy per workgroup, which keeps the
 //    register budget at two waves per SIMD for hd 128.
-//  * The 4 waves merge their (m, l, O) through LDS before the partial is written.
+//  * The waves merge their (m, l, O) through LDS before the partial is written: a tree at
+//    four waves, and at eight a flat merge (all hand over at once, each wave then folds the
+//    eight slots for its share of the dims and writes those dims).
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -324,8 +326,9 @@ decode_part_kernel(DecodeArgs a)
         step(I1{}, s + 1);
     }
 
-    // ---- row sums across the four lanes of a row, then merge the NW waves in LDS (a tree:
-    // the upper half of the waves hands its (O, m, l) to the lower half, log2 NW times)
+    // ---- row sums across the four lanes of a row, then merge the NW waves in LDS (four
+    // waves: a tree, the upper half handing its (O, m, l) to the lower half, log2 NW times;
+    // eight: the flat merge below)
     float lt[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
