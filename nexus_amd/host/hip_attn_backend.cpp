@@ -61,6 +61,7 @@ HipAttnBackend::~HipAttnBackend()
         if (m.second.k.ptr) (void)hipFree(m.second.k.ptr);
         if (m.second.v.ptr) (void)hipFree(m.second.v.ptr);
     }
+    if (ws_done_) (void)hipEventDestroy((hipEvent_t)ws_done_);
     if (stream_) (void)hipStreamDestroy((hipStream_t)stream_);
 }
 
@@ -76,7 +77,13 @@ bool HipAttnBackend::init(int device)
     if (hipSetDevice(device) != hipSuccess) return false;
     hipStream_t s = nullptr;
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return false;
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipStreamDestroy(s);
+        return false;
+    }
     stream_ = s;
+    ws_done_ = ev;
     device_ = device;
     ready_ = true;
     return true;
@@ -115,6 +122,22 @@ bool HipAttnBackend::ensure(DevBuf& b, size_t bytes, bool zero)
     return true;
 }
 
+bool HipAttnBackend::ws_acquire(void* stream)
+{
+    // the event is recorded after every launch that used ws_, on the stream it ran on; an
+    // event never recorded is complete, so the first wait is free
+    return hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)ws_done_, 0) == hipSuccess;
+}
+
+void HipAttnBackend::ws_release(void* stream)
+{
+    if (hipEventRecord((hipEvent_t)ws_done_, (hipStream_t)stream) != hipSuccess) {
+        // without the event the next user cannot be ordered after this one: wait here
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize((hipStream_t)stream);
+    }
+}
+
 bool HipAttnBackend::run_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
                                 const uint16_t* v, void* out, int n_splits, bool decode, void* stream)
 {
@@ -123,9 +146,11 @@ bool HipAttnBackend::run_device(const nexus_attn_desc& d, const void* q, const u
                                    : nexus_hip_attn_prefill_ws_bytes(&d);
     if (decode && ws_bytes == 0) return decline(nexus_hip_attn_last_error());
     if (!ensure(ws_, ws_bytes, /*zero=*/true)) return decline("workspace allocation failed");
+    if (!ws_acquire(stream)) return decline("hipStreamWaitEvent failed");
     const int rc = decode
         ? nexus_hip_attn_decode(&d, q, k, v, out, (float*)ws_.ptr, n_splits, (nexus_stream_t)stream)
         : nexus_hip_attn_prefill(&d, q, k, v, out, ws_.ptr, ws_.bytes, (nexus_stream_t)stream);
+    ws_release(stream);
     if (rc != NEXUS_OK) return decline(nexus_hip_attn_last_error());
     ++calls_run_;
     return true;
@@ -523,9 +548,11 @@ bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const 
     }
     // ---- split-KV attention over the mirror, output gate fused into the combine
     ad.kv_row_stride = (int64_t)m.cap;
+    if (!ws_acquire(s)) return decline("hipStreamWaitEvent failed");
     rc = nexus_hip_attn_decode_gated(&ad, q_d, (const uint16_t*)m.k.ptr, (const uint16_t*)m.v.ptr,
                                      d.has_gate ? gate_d : nullptr, attn_out, (float*)ws_.ptr, splits,
                                      (nexus_stream_t)s);
+    ws_release(s);
     if (rc != NEXUS_OK) return decline(nexus_hip_attn_last_error());
     if (hipMemcpyAsync(kv_out_host, kv_d, kv_bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)

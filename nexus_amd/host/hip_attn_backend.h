@@ -87,7 +87,9 @@ public:
                              const void* k_flat, const void* v_flat);
 
     // ---- device-resident forms (device pointers, stream-ordered, no host copies) ----
-    // The workspace is the backend's own (one call in flight per backend at a time).
+    // The split workspace is the backend's own: every launch that uses it first waits (on
+    // its stream) for the previous user, whichever stream that ran on, so calls on
+    // different streams take turns on it instead of overwriting partials still being read.
     bool prefill_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
                         const uint16_t* v, void* out, nexus_stream_t stream);
     bool decode_device(const nexus_attn_desc& d, const void* q, const uint16_t* k,
@@ -184,6 +186,10 @@ private:
     int device_ = -1;
     void* stream_ = nullptr;                 // hipStream_t
     DevBuf q_, k_, v_, o_, ws_;
+    void* ws_done_ = nullptr;                // hipEvent_t recorded after the last launch using ws_
+    // Order a launch that uses ws_ on `stream` after the previous one, and record it.
+    bool ws_acquire(void* stream);
+    void ws_release(void* stream);
     long long calls_run_ = 0, calls_declined_ = 0;
     const char* last_decline_ = "";
 };

@@ -52,6 +52,17 @@ def make_desc_for(q: torch.Tensor, k: torch.Tensor, *, n_kv_heads: int, q_base_p
                           softcap=softcap, q_dtype=_DT[q.dtype], o_dtype=_DT[od])
 
 
+def _check_out(out: torch.Tensor, q: torch.Tensor) -> None:
+    """A caller-supplied output must be exactly what the kernels write: a contiguous tensor
+    shaped like q on q's device, f32 or f16 (the kernels store n_query * Hq * hd elements)."""
+    if not isinstance(out, torch.Tensor) or not out.is_cuda or out.device != q.device:
+        raise ValueError("out must be a device tensor on q's device")
+    if out.dtype not in _DT:
+        raise ValueError(f"out dtype {out.dtype} not supported (float32 or float16)")
+    if tuple(out.shape) != tuple(q.shape) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous and shaped like q {tuple(q.shape)}, got {tuple(out.shape)}")
+
+
 def _gate_ptr(gate: torch.Tensor | None, q: torch.Tensor) -> int:
     if gate is None:
         return 0
@@ -70,6 +81,8 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_head
     output by sigmoid(gate) clamped at +-80 (nexus_hip_attn_prefill_gated)."""
     _check_tensors(q, k, v, n_kv_heads)
     gate_ptr = _gate_ptr(gate, q)
+    if out is not None:
+        _check_out(out, q)
     desc = make_desc_for(q, k, n_kv_heads=n_kv_heads, q_base_pos=q_base_pos, n_ctx=n_ctx,
                          sliding_window=sliding_window, scale=scale, softcap=softcap,
                          out_dtype=out_dtype if out is None else out.dtype)
@@ -97,9 +110,11 @@ def attn_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, n_kv_heads
     """Split-KV decode / verify (nexus_hip_attn_decode); `gate` as in attn_prefill."""
     _check_tensors(q, k, v, n_kv_heads)
     gate_ptr = _gate_ptr(gate, q)
+    if out is not None:
+        _check_out(out, q)
     desc = make_desc_for(q, k, n_kv_heads=n_kv_heads, q_base_pos=q_base_pos, n_ctx=n_ctx,
                          sliding_window=sliding_window, scale=scale, softcap=softcap,
-                         out_dtype=out_dtype or (out.dtype if out is not None else torch.float32))
+                         out_dtype=out.dtype if out is not None else (out_dtype or torch.float32))
     if out is None:
         out = torch.empty(q.shape, dtype=out_dtype or torch.float32, device=q.device)
     need = capi.decode_ws_bytes(desc, n_splits)

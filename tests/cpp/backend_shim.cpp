@@ -90,6 +90,22 @@ int shim_kv_mirror_read(const void* owner, int layer, int kv_head, int pos0, int
     return backend().kv_mirror_read(owner, layer, kv_head, pos0, n, k_out, v_out) ? 1 : 0;
 }
 
+// device-resident forms: device pointers, the caller's stream (a hipStream_t as void*)
+int shim_prefill_device(const nexus_attn_desc* d, const void* q, const void* k, const void* v, void* out,
+                        void* stream)
+{
+    return backend().prefill_device(*d, q, (const uint16_t*)k, (const uint16_t*)v, out, (nexus_stream_t)stream) ? 1
+                                                                                                                 : 0;
+}
+int shim_decode_device(const nexus_attn_desc* d, const void* q, const void* k, const void* v, void* out,
+                       int n_splits, void* stream)
+{
+    return backend().decode_device(*d, q, (const uint16_t*)k, (const uint16_t*)v, out, n_splits,
+                                   (nexus_stream_t)stream)
+               ? 1
+               : 0;
+}
+
 long long shim_calls_run(void) { return backend().calls_run(); }
 long long shim_calls_declined(void) { return backend().calls_declined(); }
 const char* shim_last_decline(void) { return backend().last_decline(); }

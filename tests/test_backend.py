@@ -38,6 +38,9 @@ def shim():
                                              ctypes.c_size_t]
     lib.shim_attention_stream_gpu.argtypes = [_f32p, _f32p, _i, _i, _i, _i, _i, _i, _f, _f, _u16p, _u16p, _i]
     lib.shim_attention_flash_gpu.argtypes = [_f32p, _f32p, _i, _i, _i, _i, _i, _i, _i, _f, _f, _u16p, _u16p]
+    vp = ctypes.c_void_p
+    lib.shim_prefill_device.argtypes = [vp, vp, vp, vp, vp, vp]
+    lib.shim_decode_device.argtypes = [vp, vp, vp, vp, vp, _i, vp]
     lib.shim_calls_run.restype = ctypes.c_longlong
     lib.shim_calls_declined.restype = ctypes.c_longlong
     lib.shim_last_decline.restype = ctypes.c_char_p
@@ -148,3 +151,53 @@ def test_backend_declines_like_the_reference(hip):
     finally:
         del os.environ["NEXUS_FLASH_KV_MB"]
     assert lib.shim_attention_flash_gpu(q, out, 8, 2, 64, 20, 5, 15, 0, 0.0, 0.0, k, v) == 1
+
+
+@pytest.mark.gpu
+def test_device_forms_on_two_streams_take_turns_on_the_workspace(hip):
+    """prefill_device and decode_device share the backend's split workspace.  Launched back to
+    back on two different streams with no synchronisation between them, the second call's
+    partials must not overwrite the first call's while its combine still reads them: every
+    output matches the oracle."""
+    import torch
+
+    from nexus_amd import capi
+
+    lib = shim()
+    assert lib.shim_ready() == 1
+
+    def dev(x):
+        if x.dtype == np.uint16:
+            return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).cuda()
+        return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+    # a short chunk over a long cache (split prefill + combine) and a 64-split decode
+    pq, pk, pv = make_case(n_q_heads=8, n_kv_heads=2, head_dim=128, n_query=64, n_ctx=8064, seed=61)
+    pdesc = capi.make_desc(n_q_heads=8, n_kv_heads=2, head_dim=128, n_query=64, q_base_pos=8000, n_ctx=8064)
+    dq, dk, dv = make_case(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=1, n_ctx=20000, seed=62)
+    ddesc = capi.make_desc(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=1, q_base_pos=19999, n_ctx=20000)
+    assert capi.prefill_ws_bytes(pdesc) > 0
+    pref = O.attn_batch(pq, pk, pv, n_kv_heads=2, n_ctx=8064, q_base_pos=8000, n_threads=8)
+    dref = O.attn_batch(dq, dk, dv, n_kv_heads=8, n_ctx=20000, q_base_pos=19999, n_threads=8)
+    pqd, pkd, pvd, dqd, dkd, dvd = map(dev, (pq, pk, pv, dq, dk, dv))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    # size the backend's workspace for the larger of the two calls first
+    pout = torch.empty(pq.shape, device="cuda")
+    dout = torch.empty(dq.shape, device="cuda")
+    for d, call in ((pdesc, lambda st: lib.shim_prefill_device(ctypes.byref(pdesc), pqd.data_ptr(), pkd.data_ptr(),
+                                                                pvd.data_ptr(), pout.data_ptr(), st.cuda_stream)),
+                    (ddesc, lambda st: lib.shim_decode_device(ctypes.byref(ddesc), dqd.data_ptr(), dkd.data_ptr(),
+                                                               dvd.data_ptr(), dout.data_ptr(), 64, st.cuda_stream))):
+        assert call(s1) == 1, lib.shim_last_decline()
+    torch.cuda.synchronize()
+    for it in range(8):
+        pout.fill_(float("nan"))
+        dout.fill_(float("nan"))
+        torch.cuda.synchronize()
+        assert lib.shim_prefill_device(ctypes.byref(pdesc), pqd.data_ptr(), pkd.data_ptr(), pvd.data_ptr(),
+                                       pout.data_ptr(), s1.cuda_stream) == 1
+        assert lib.shim_decode_device(ctypes.byref(ddesc), dqd.data_ptr(), dkd.data_ptr(), dvd.data_ptr(),
+                                      dout.data_ptr(), 64, s2.cuda_stream) == 1
+        torch.cuda.synchronize()
+        assert_close(pout.cpu().numpy(), pref, f"prefill_device on stream 1, round {it}")
+        assert_close(dout.cpu().numpy(), dref, f"decode_device on stream 2, round {it}")
