@@ -66,7 +66,7 @@ enum nexus_status {
 typedef struct nexus_attn_desc {
     int32_t n_q_heads;       /* Hq  (> 0, multiple of n_kv_heads)                    */
     int32_t n_kv_heads;      /* Hkv (> 0)                                            */
-    int32_t head_dim;        /* 64, 128 or 256 (reference: hd % 64 == 0, hd <= 256) */
+    int32_t head_dim;        /* 64, 128, 192 or 256 (reference: hd % 64 == 0, <= 256) */
     int32_t n_query;         /* queries in this call (> 0)                           */
     int32_t q_base_pos;      /* absolute position of query 0 (>= 0)                  */
     int32_t n_ctx;           /* keys [0, n_ctx) are valid in K/V (> 0)               */
@@ -129,6 +129,22 @@ int nexus_hip_attn_decode_gated(const nexus_attn_desc* desc,
                                 const float* gate, void* out,
                                 float* partial_ws, int n_splits,
                                 nexus_stream_t stream);
+
+/* Allocation-free decode.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  nexus_hip_attn_decode_gated with the split partials in a fixed
+ * device array of NEXUS_DECODE_NOALLOC_SCRATCH_BYTES that the library keeps on every GPU
+ * it runs on until the process ends, instead of a caller workspace; it calls no hipMalloc,
+ * hipFree or allocating library routine.  n_splits <= 0: the default split count, lowered
+ * until the partials fit; an explicit n_splits whose partials exceed the array returns
+ * NEXUS_E_WORKSPACE with nothing launched.  All calls on one GPU share the array: calls
+ * that overlap on one GPU (several streams at once) race on it, so keep one in flight per
+ * GPU.  The first call on a device looks up that device's array address. */
+#define NEXUS_DECODE_NOALLOC_SCRATCH_BYTES (8u << 20)
+int nexus_hip_attn_decode_noalloc(const nexus_attn_desc* desc,
+                                  const void* q, const uint16_t* k, const uint16_t* v,
+                                  const float* gate, void* out, int n_splits,
+                                  nexus_stream_t stream);
 
 /* Decode prep for one token, the step before the decode call in the gated (and plain)
  * full-attention layers: per-head RMSNorm of q and k, RoPE over the first rot_dims dims

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "nexus_hip_attn_prefill_gated",
     "nexus_hip_attn_decode_gated",
     "nexus_hip_attn_decode_prep",
+    "nexus_hip_attn_decode_noalloc",
     "nexus_hip_kv_layer_bytes",
     "nexus_hip_kv_cache_bytes",
     "nexus_hip_kv_layer_save",
@@ -148,6 +149,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.nexus_hip_attn_prefill_gated.restype = ctypes.c_int
     lib.nexus_hip_attn_decode_gated.argtypes = [dp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
     lib.nexus_hip_attn_decode_gated.restype = ctypes.c_int
+    lib.nexus_hip_attn_decode_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
+    lib.nexus_hip_attn_decode_noalloc.restype = ctypes.c_int
     lib.nexus_hip_attn_decode_prep.argtypes = [ctypes.POINTER(PrepDesc)] + [vp] * 12
     lib.nexus_hip_attn_decode_prep.restype = ctypes.c_int
     kvp = ctypes.POINTER(KvLayerView)
@@ -217,6 +220,17 @@ def decode_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, ws: int, n_spli
         rc = lib.nexus_hip_attn_decode_gated(ctypes.byref(desc), q, k, v, gate, out, ws, int(n_splits), stream)
     else:
         rc = lib.nexus_hip_attn_decode(ctypes.byref(desc), q, k, v, out, ws, int(n_splits), stream)
+    return _check(rc) if check else rc
+
+
+# Size of the device array behind nexus_hip_attn_decode_noalloc (include/nexus_hip_attn.h).
+DECODE_NOALLOC_SCRATCH_BYTES = 8 << 20
+
+
+def decode_noalloc_raw(desc: AttnDesc, q: int, k: int, v: int, out: int, n_splits: int, stream: int,
+                       check: bool = True, gate: int = 0) -> int:
+    """nexus_hip_attn_decode_noalloc: the gated decode with the library's fixed partial array."""
+    rc = load().nexus_hip_attn_decode_noalloc(ctypes.byref(desc), q, k, v, gate or None, out, int(n_splits), stream)
     return _check(rc) if check else rc
 
 

@@ -9,6 +9,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -291,6 +292,27 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
 
 }  // namespace
 
+int nxa::decode_into(const nexus_attn_desc* desc, const void* q, const uint16_t* k, const uint16_t* v,
+                     const float* gate, void* out, float* ws, size_t ws_cap, int n_splits, hipStream_t stream)
+{
+    const int rc = check_desc(desc);
+    if (rc != NEXUS_OK) return rc;
+    if (!q || !k || !v || !out) return capi_fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
+    if (gate && ((uintptr_t)gate & 15u)) return capi_fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
+    if (n_splits > kMaxSplits) return capi_fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
+    if (n_splits <= 0) {
+        n_splits = default_decode_splits(desc);
+        const size_t per_split = decode_ws_bytes(desc, 1);
+        if (n_splits > 1 && decode_ws_bytes(desc, n_splits) > ws_cap)
+            n_splits = per_split > 0 ? (int)std::max<size_t>(1, ws_cap / per_split) : 1;
+    }
+    // one split writes `out` directly and touches no partials
+    if (n_splits > 1 && (!ws || decode_ws_bytes(desc, n_splits) > ws_cap))
+        return capi_fail(NEXUS_E_WORKSPACE, "n_splits=%d needs %zu bytes of partials, the workspace holds %zu",
+                         n_splits, decode_ws_bytes(desc, n_splits), ws_cap);
+    return run_decode(desc, q, k, v, out, gate, ws, n_splits, stream);
+}
+
 extern "C" {
 
 size_t nexus_hip_attn_decode_ws_bytes(const nexus_attn_desc* desc, int n_splits)
@@ -313,12 +335,11 @@ int nexus_hip_attn_decode_gated(const nexus_attn_desc* desc, const void* q, cons
 {
     const int rc = check_desc(desc);
     if (rc != NEXUS_OK) return rc;
-    if (!q || !k || !v || !out) return capi_fail(NEXUS_E_INVALID, "null q/k/v/out pointer");
     if (!partial_ws) return capi_fail(NEXUS_E_WORKSPACE, "partial_ws is NULL");
-    if (gate && ((uintptr_t)gate & 15u)) return capi_fail(NEXUS_E_INVALID, "gate is not 16-byte aligned");
-    if (n_splits <= 0) n_splits = default_decode_splits(desc);
-    if (n_splits > kMaxSplits) return capi_fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
-    return run_decode(desc, q, k, v, out, gate, partial_ws, n_splits, (hipStream_t)stream);
+    // the caller sized partial_ws for this split count (nexus_hip_attn_decode_ws_bytes)
+    const int s = n_splits <= 0 ? default_decode_splits(desc) : n_splits;
+    return nxa::decode_into(desc, q, k, v, gate, out, partial_ws, s <= kMaxSplits ? decode_ws_bytes(desc, s) : 0,
+                            s, (hipStream_t)stream);
 }
 
 int nexus_hip_attn_decode(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
