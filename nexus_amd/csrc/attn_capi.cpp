@@ -122,14 +122,11 @@ long long decode_rows(const nexus_attn_desc* d)
     return (long long)d->n_query * (d->n_q_heads / d->n_kv_heads);
 }
 
-// 16-row tiles per workgroup: two when the rows need more than one tile, so a 32-row
-// verify batch (4 drafts x 8 heads) shares every K/V byte it reads.
-// Two 16-row tiles per workgroup up to head dim 128 (one K/V read feeds 32 rows); above that
-// one tile and more row groups, which keeps two waves per SIMD (the row groups of a split
-// read the same keys, through the XCD's L2 -- see default_decode_splits).
+// 16-row tiles per workgroup: two when the rows need more than one tile, so a 32-row verify
+// batch (4 drafts x 8 heads) shares every K/V byte the workgroup stages.
 int decode_row_tiles(const nexus_attn_desc* d)
 {
-    return decode_rows(d) > nxa::kDecodeRowTile && d->head_dim <= 128 ? nxa::kDecodeMaxRowTiles : 1;
+    return decode_rows(d) > nxa::kDecodeRowTile ? nxa::kDecodeMaxRowTiles : 1;
 }
 
 int decode_rowgroups(const nexus_attn_desc* d)
@@ -138,12 +135,8 @@ int decode_rowgroups(const nexus_attn_desc* d)
     return (int)((decode_rows(d) + per - 1) / per);
 }
 
-// Workgroups resident at once per CU for the decode kernel (its register budget).
-int decode_wg_per_cu(const nexus_attn_desc* d)
-{
-    if (nxa::decode_waves(d->head_dim, decode_row_tiles(d)) == 8) return 1;   // 8 waves: one per CU
-    return d->head_dim * decode_row_tiles(d) <= 256 ? 2 : 1;     // decode_waves_per_simd
-}
+// Keys per split at least: two 32-key stages of the ring.
+constexpr long long kDecodeMinSplitKeys = 64;
 
 int default_decode_splits(const nexus_attn_desc* d)
 {
@@ -151,26 +144,15 @@ int default_decode_splits(const nexus_attn_desc* d)
     key_range(d, &kb, &ke);
     const long long kv_len = ke - kb;
     const long long base = (long long)d->n_kv_heads * decode_rowgroups(d);
-    // About one workgroup per CU above head dim 128, two up to it: a split of a 256-dim
-    // head is only one or two K/V steps per wave at 2 per CU, and its fixed cost (Q staging,
-    // the cross-wave merge, the partial) then outweighs the extra streams -- measured on
-    // MI355X at 32k keys: 16q/2kv hd256 fastest at 128 splits (1 query) / 64 (4 drafts).
-    const long long target = (long long)(d->head_dim > 128 ? 1 : decode_wg_per_cu(d)) * device_cus();
+    // as many workgroups as are resident at once (one wave of the grid): a second wave would
+    // pay the per-workgroup start (Q load, ring prologue) and the partial again
+    const long long target = (long long)nxa::decode_wg_per_cu(d->head_dim) * device_cus();
     long long s = target / base;
     if (s < 1) s = 1;
-    const long long by_len = (kv_len + 127) / 128;           // keep >= 128 keys (one step per wave)
+    const long long by_len = (kv_len + kDecodeMinSplitKeys - 1) / kDecodeMinSplitKeys;
     if (s > by_len) s = by_len;
     if (s < 1) s = 1;
     if (s > kMaxSplits) s = kMaxSplits;
-    // Several row groups: workgroups are dealt to the 8 XCDs round-robin in grid order
-    // (split fastest, row group slowest), so the row groups of one (split, kv head) share an
-    // XCD -- and its L2 copy of their keys -- when splits x kv heads is a multiple of 8.
-    if (decode_rowgroups(d) > 1) {
-        long long m = 8;
-        for (long long h = d->n_kv_heads; h % 2 == 0 && m > 1; h /= 2) m /= 2;
-        s = (s + m - 1) / m * m;
-        if (s > kMaxSplits) s = kMaxSplits / m * m;
-    }
     return (int)s;
 }
 

@@ -2,540 +2,510 @@
 //
 // Two passes, as the reference's decode split-K (src/gpu/shaders/qwen35_attn_part.comp and
 // qwen35_attn_comb.comp, dispatched back to back at src/gpu/vulkan_backend.h:5462-5482):
-//  * decode_part_kernel: one workgroup per (split, kv head, row group) streams its slice of
+//  * decode_ring_kernel: one workgroup per (split, kv head, row group) streams its slice of
 //    the cache once and writes, for every query row, acc[hd] = sum_k e^{s_k - m} v_k,
 //    m (the split's max scaled score) and l = sum_k e^{s_k - m} to
 //    part[row][split][hd + 2] -- the reference's partial format (qwen35_attn_part.comp:3).
 //    With one split it writes the normalised output directly.
-//  * combine_kernel: out = sum_c acc_c e^{m_c - M} / sum_c l_c e^{m_c - M}, M = max_c m_c
-//    (qwen35_attn_comb.comp:16-40, without the output gate).
-// The kernel boundary makes the partials visible to the combine; an in-kernel
-// "last workgroup merges" scheme needs an agent-scope release per workgroup, which
-// writes back the XCD's L2 each time and measured slower than the second launch.
+//  * combine_slices_kernel: out = sum_c acc_c e^{m_c - M} / sum_c l_c e^{m_c - M},
+//    M = max_c m_c (qwen35_attn_comb.comp:16-40), output gate included.
 //
 // Rows are (draft i, q head g of the GQA group) pairs, row = i * G + g, so every K/V byte a
-// workgroup reads feeds all G heads of the group and all drafts of a speculative verify.
+// workgroup reads feeds all G heads of the group and all drafts of a speculative verify (up
+// to 32 rows per workgroup; more rows take more row groups).
 //
-// Per wave and 32-key step (4 waves take interleaved steps of the split):
-//  * K rows go from HBM straight into MFMA A-operand registers (non-temporal 16-byte
-//    buffer loads, 64 contiguous bytes per key per instruction).  S^T = K Q^T on
-//    v_mfma_f32_16x16x32_f16, 16 query rows per row tile (RT tiles per wave).  f32
-//    queries are split into an f16 high part and an f16 residual (two MFMAs), so scores
-//    carry ~22 mantissa bits like the reference's f32 dot products.
-//  * The 32 keys of a step form two 16-key S^T tiles whose rows are the keys
-//    8*(r/4) + 4*t + (r%4) (tile t, row r).  The D layout then leaves lane (row n, group g)
-//    holding keys 8g..8g+7 of row n -- exactly the B operand of O^T += V^T P^T, so P
-//    needs no shuffle.  Row max/sum: v_permlane16_swap + v_permlane32_swap on the VALU.
-//  * V rows are transposed into a wave-private LDS region (v_perm, 8-byte writes) and read
-//    back as V^T A operands (16 bytes = 8 keys of one dim).
-//  * Software pipeline over register double buffers: K and V of step s + 2 are issued as
-//    soon as step s has consumed its K and V registers, so two steps (32 KB at hd 128) stay
-//    in flight per wave (one step from hd x rows > 128, with two waves per SIMD).  The Q^T
-//    operands (f16 high/low parts) sit in LDS, one copy per workgroup, which keeps the
-//    register budget at two waves per SIMD for hd 128.
-//  * The waves merge their (m, l, O) through LDS before the partial is written: a tree at
-//    four waves, and at eight a flat merge (all hand over at once, each wave then folds the
-//    eight slots for its share of the dims and writes those dims).
+// The ring kernel:
+//  * K and V go HBM -> LDS with buffer-load-to-LDS into a ring of NSTAGE stages of 32 keys
+//    (48-96 KB per workgroup): no register holds data in flight, so a workgroup keeps
+//    NSTAGE - 1 stages (32-64 KB) of loads outstanding.  Every thread loads its share of each
+//    stage; per stage: wait for the own loads (vmcnt), one s_barrier, refill the slot the
+//    previous stage used, compute.  16-byte chunks are XOR-swizzled per row, each lane picking
+//    the global chunk for its LDS slot, so both operand reads below are free of bank conflicts.
+//  * Waves split the work, not the keys: wave w takes row tile w / DG (16 query rows) and the
+//    dims [w % DG * HD / DG, ...) of the output, DG = 4 / row tiles.  The DG waves of a row tile
+//    split the score reduction S^T = K Q^T over head dims (k-steps dg, dg + DG, ... of 32 dims
+//    each, on v_mfma_f32_16x16x32_f16), exchange the partial scores through LDS and add them
+//    in one fixed order, so all DG waves hold bit-identical scores, m and l; each then does
+//    O^T += V^T P^T for its own dims.  The waves never merge (m, l, O) with each other: each
+//    writes its own dims.  f32 queries are split into an f16 high part and an f16 residual
+//    (two MFMAs), so scores carry ~22 mantissa bits like the reference's f32 dot products;
+//    f16 queries are used as given.
+//  * Rows past n_rows (a 16-row tile with fewer real rows) compute with zero queries and are
+//    never written; masks apply only to stages that hold an invisible key for some row.
+//  * The two 16-key S^T tiles of a stage hold the keys 8*(r/4) + 4*t + (r%4) (tile t, row r),
+//    so the MFMA result leaves lane (query row n, group g) with keys 8g .. 8g+7 of row n --
+//    exactly the B operand of O^T += V^T P^T: P needs no shuffle.  V^T operands come from LDS
+//    with ds_read_b64_tr_b16 (two transposing reads = 8 keys of one dim).
+#include <climits>
+
 #include "attn_common.h"
 #include "attn_kernels.h"
 
 namespace nxa {
 
-// Register budget per (head_dim x row tiles): two waves per SIMD up to 256 (two steps of K/V
-// in flight up to 128, one step above); one wave per SIMD beyond, which the host avoids for
-// head dims above 128 by using one row tile and more row groups (at one wave per SIMD the
-// compiler moves the accumulators through AGPRs on every step).
-constexpr int decode_waves_per_simd(int hd, int rt) { return hd * rt <= 256 ? 2 : 1; }
-constexpr int decode_depth(int hd, int rt) { return hd * rt <= 128 ? 2 : (hd * rt <= 256 ? 1 : (hd * rt <= 384 ? 2 : 1)); }
+namespace {
 
-template <int HD, int RT>
-struct DecodeLayout {
-    static constexpr int NW = decode_waves(HD, RT);               // waves per workgroup
-    static constexpr int KEYS = kDecodeKeys;                  // 32 keys per wave step
-    static constexpr int KS = HD / 32;                        // 32-dim k-steps of S^T
-    static constexpr int DT = HD / 16;                        // 16-dim tiles of O^T
-    static constexpr int VB = (KEYS / 4) * (HD / 8) / 64;     // (4-key, 8-dim) V blocks per lane
-    static constexpr int VT_WAVE = HD * KEYS * 2;             // V^T bytes per wave
-    static constexpr int DEPTH = decode_depth(HD, RT);        // steps of K/V in flight
-    static constexpr int Q_BYTES = RT * KS * 2 * 64 * 16;     // Q^T operands (hi, lo) per workgroup
-    static constexpr int OREGS = RT * DT * 4;                 // f32 O^T values per lane
-    static constexpr int MERGE_SLOT = (OREGS + 2 * RT) * 64 * 4;
-    // merge: a tree through NW / 2 slots at four waves; at eight, every wave's slot at once
-    // (one barrier, then each wave folds all eight for its share of the dims)
-    static constexpr bool FLAT_MERGE = NW == 8;
-    static constexpr int MERGE_BYTES = (FLAT_MERGE ? NW : NW / 2) * MERGE_SLOT;
-    static constexpr int MAIN_BYTES = NW * VT_WAVE > MERGE_BYTES ? NW * VT_WAVE : MERGE_BYTES;
-    static constexpr int LDS_BYTES = MAIN_BYTES + Q_BYTES;
-    static_assert(VB >= 1 && (KEYS / 4) * (HD / 8) % 64 == 0, "V staging");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+template <int HD>
+struct RingLayout {
+    static constexpr int ROW = HD * 2;                          // bytes per K/V row
+    static constexpr int SK = kDecodeKeys;                      // keys per stage
+    static constexpr int STAGE = SK * ROW;                      // bytes per stage per operand
+    static constexpr int NL = STAGE / (kDecodeThreads * 16);    // 16-byte loads per thread per operand
+    // ring depth: two or three stages in flight while one is computed (measured on MI355X: a
+    // fourth stage at head dims 128 and 256 makes the calls 1-3% slower); 48-64 KB per workgroup
+    // at two workgroups per CU (head dims <= 128), 96 KB at one per CU above
+    static constexpr int NSTAGE = HD <= 64 ? 8 : (HD <= 128 ? 3 : (HD <= 192 ? 4 : 3));
+    static constexpr int WG_PER_CU = decode_wg_per_cu(HD);
+    static constexpr int VBASE = NSTAGE * STAGE;
+    static constexpr int XBASE = 2 * NSTAGE * STAGE;            // partial scores: [wave][tile][lane] f32x4
+    static constexpr int LDS_BYTES = XBASE + 4 * 2 * 64 * 16;
+    static constexpr int KS = HD / 32;                          // 32-dim k-steps of S^T
+    static constexpr int CPR = HD / 8;                          // 16-byte chunks per row
+    static constexpr int KSWZ = CPR % 16 == 0 ? 15 : 7;         // K chunk swizzle mask
+    static constexpr int LPS = 2 * NL;                          // loads per thread per stage
+    static_assert(STAGE % (kDecodeThreads * 16) == 0 && NL >= 1, "stage staging");
+    static_assert(LDS_BYTES * WG_PER_CU <= 160 * 1024, "LDS budget");
+    static_assert((NSTAGE - 2) * LPS <= 63, "vmcnt range");
 };
 
-// V^T byte offset: dim row d (64-byte rows of 32 keys), 8-key chunk c, 4-key half h.  The
-// chunk is XOR-swizzled with bits 1-2 of the row, so the 16 rows an operand read touches
-// (16*dt + 0..15, same chunk) fall on distinct banks within every 8 lanes.
-__device__ __forceinline__ int vt_off(int d, int c, int h)
+// Swizzled slot of K chunk c of row r: rows 8*(n/4) + 4t + (n%4) of a score tile (n = 0..15)
+// get slot c ^ n, so the 16 lanes of an operand read hit 16 different 16-byte slots.
+template <int HD>
+__device__ __forceinline__ int rk_slot(int r, int c)
 {
-    return d * (kDecodeKeys * 2) + 16 * (c ^ ((d >> 1) & 3)) + 8 * h;
+    return c ^ (((r & 3) | (((r >> 3) & 3) << 2)) & RingLayout<HD>::KSWZ);
 }
+// Swizzled slot of V chunk c of row r: the four rows of a transposing read (r % 4 = 0..3) land
+// 32 bytes apart within one 128-byte span.
+__device__ __forceinline__ int rv_slot(int r, int c) { return c ^ (2 * (r & 3)); }
 
 constexpr int kAuxNT = 2;   // buffer-load cache policy: non-temporal (streaming K/V)
 
-__device__ __forceinline__ u32x4 buf_load16_nt(rsrc_t r, uint32_t byte_off)
+// LDS reads as inline asm: the compiler cannot tell the ring slots apart from the slots the
+// buffer-load-to-LDS writes are filling, and would wait for all of them before a plain LDS
+// load.  Each read is waited for explicitly (lgkm_wait); a wave's LDS operations complete in
+// order.
+__device__ __forceinline__ u32x4 lds_b128(const lds_u8* p)
 {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kAuxNT));
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(p) : "memory");
+    return r;
 }
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_tr16(const lds_u8* p)
+{
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(p), "i"(OFF) : "memory");
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait(u32x4& a)
+{
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait(u32x2& a, u32x2& b)
+{
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void vm_wait()
+{
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+}  // namespace
 
 template <int HD, int RT, bool Q_F32, bool O_F32, bool EXT>
-__global__ void __launch_bounds__(64 * decode_waves(HD, RT), decode_waves_per_simd(HD, RT))
-decode_part_kernel(DecodeArgs a)
+__global__ void __launch_bounds__(kDecodeThreads, decode_wg_per_cu(HD))
+decode_ring_kernel(DecodeArgs a)
 {
-    using L = DecodeLayout<HD, RT>;
-    constexpr int NW = L::NW;
-    constexpr int KS = L::KS, DT = L::DT, VB = L::VB;
+    using L = RingLayout<HD>;
+    constexpr int KS = L::KS, ROW = L::ROW, NSTAGE = L::NSTAGE;
+    constexpr int DG = 4 / RT;                                  // dim groups per row tile
+    constexpr int DTW = HD / DG / 16;                           // 16-dim output tiles per wave
+    constexpr int KSW = (KS + DG - 1) / DG;                     // score k-steps per wave (at most)
+    static_assert(DTW >= 1 && HD % (16 * DG) == 0, "dims per wave");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    lds_u8* lds3 = (lds_u8*)lds;
 
-    // the wave index is uniform across the wave: readfirstlane lets the compiler keep
-    // per-wave bounds and branches scalar
+    // the wave index is uniform across the wave: readfirstlane keeps per-wave values scalar
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
+    const int rt = wave / DG, dg = wave % DG;
     const int split = blockIdx.x, kvh = blockIdx.y, rg = blockIdx.z;
 
-    // ---- query rows of this lane's columns: R = draft * G + head-in-group
-    int R[RT], qi[RT], h[RT], khi[RT], klo[RT];
-    bool rok[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        R[rt] = rg * (16 * RT) + 16 * rt + n;
-        rok[rt] = R[rt] < a.n_rows;
-        qi[rt] = rok[rt] ? R[rt] / a.group : 0;
-        h[rt] = kvh * a.group + (rok[rt] ? R[rt] - qi[rt] * a.group : 0);
-        const int qpos = a.q_base + qi[rt];
-        khi[rt] = min(qpos, a.n_ctx - 1);
-        klo[rt] = (EXT && a.sliding_window > 0 && qpos + 1 > a.sliding_window) ? qpos + 1 - a.sliding_window : 0;
-    }
+    // ---- this lane's query row (as an MFMA column): R = draft * G + head-in-group.  A row
+    // past n_rows computes with a zero query, is never written, and is not masked.
+    const int R = rg * (16 * RT) + 16 * rt + n;
+    const bool rok = R < a.n_rows;
+    const int qi = rok ? R / a.group : 0;
+    const int h = kvh * a.group + (rok ? R - qi * a.group : 0);
+    const int qpos = a.q_base + qi;
+    const int khi = rok ? min(qpos, a.n_ctx - 1) : INT_MAX;
+    const int klo = (EXT && rok && a.sliding_window > 0 && qpos + 1 > a.sliding_window) ? qpos + 1 - a.sliding_window : 0;
 
-    // ---- Q^T B operands in LDS: lane (row n, group g) holds dims 32*ks + 8*g .. +7, as an
-    // f16 high part and (f32 queries) the f16 residual.  Wave 0 issues the Q loads before
-    // the K/V prologue and converts them once those loads are in flight, so the two
-    // latencies overlap.
-    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
-    constexpr int QV = Q_F32 ? 2 : 1;                           // 16-byte loads per operand
-    uint8_t* qlds = lds + L::MAIN_BYTES;
-    auto qslot = [&](int rt, int ks, int hl) { return qlds + (((rt * KS + ks) * 2 + hl) * 64 + lane) * 16; };
-    u32x4 qraw[RT][KS][QV];
-    if (wave == 0) {
-        const rsrc_t qr = make_rsrc_uniform(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            // rows past n_rows point past the descriptor and read as zero
-            const uint32_t qoff = rok[rt] ? (uint32_t)((((size_t)qi[rt] * a.n_q_heads + h[rt]) * HD + 8 * g) * QE)
-                                          : 0x7fffff00u;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-                for (int j = 0; j < QV; ++j) qraw[rt][ks][j] = buf_load16(qr, qoff + 32 * QE * ks + 16 * j);
-        }
-    }
-    auto store_q = [&]() {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                if constexpr (Q_F32) {
-                    const f32x4 x0 = __builtin_bit_cast(f32x4, qraw[rt][ks][0]);
-                    const f32x4 x1 = __builtin_bit_cast(f32x4, qraw[rt][ks][QV - 1]);
-                    const f16x8 hi = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
-                    *(f16x8*)qslot(rt, ks, 0) = hi;
-                    *(f16x8*)qslot(rt, ks, 1) =
-                        cvt_f16x8(x0[0] - (float)hi[0], x0[1] - (float)hi[1], x0[2] - (float)hi[2],
-                                  x0[3] - (float)hi[3], x1[0] - (float)hi[4], x1[1] - (float)hi[5],
-                                  x1[2] - (float)hi[6], x1[3] - (float)hi[7]);
-                } else {
-                    *(f16x8*)qslot(rt, ks, 0) = as_f16x8(qraw[rt][ks][0]);
-                }
-            }
-    };
-
+    // ---- keys of this workgroup
     const int s_begin = a.k_begin + split * a.chunk;
     const int s_end = min(s_begin + a.chunk, a.k_end);
-    const int n_sub = s_begin < s_end ? (s_end - s_begin + L::KEYS - 1) / L::KEYS : 0;
-    const int n_my = n_sub > wave ? (n_sub - wave + NW - 1) / NW : 0;   // steps wave, wave+NW, ...
+    const int n_st = s_begin < s_end ? (s_end - s_begin + L::SK - 1) / L::SK : 0;
 
-    // K/V of this kv head; the descriptors end at this split's last key
-    const uint32_t kv_bytes = (uint32_t)max(s_end, 0) * HD * 2;
+    // ---- Q^T B operands of this wave's k-steps ks = dg + DG * i, loaded first: lane (row n,
+    // group g) holds dims 32 ks + 8 g .. +7
+    constexpr uint32_t QE = Q_F32 ? 4u : 2u;
+    constexpr int QV = Q_F32 ? 2 : 1;
+    u32x4 qraw[KSW][QV];
+    {
+        const rsrc_t qr = make_rsrc_uniform(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
+        // rows past n_rows point past the descriptor and read as zero
+        const uint32_t qoff = rok ? (uint32_t)((((size_t)qi * a.n_q_heads + h) * HD + 8 * g) * QE) : 0x7fffff00u;
+#pragma unroll
+        for (int i = 0; i < KSW; ++i) {
+            const int ks = dg + DG * i;                         // past KS: reads beyond the row, unused
+#pragma unroll
+            for (int j = 0; j < QV; ++j) qraw[i][j] = buf_load16(qr, qoff + 32 * QE * ks + 16 * j);
+        }
+    }
+
+    // ---- ring loads: thread tid, load j fills bytes 4096 j + 16 tid of a stage's K (or V)
+    // slot; the descriptors end at this split's last key, so later rows read as zero
+    const uint32_t kv_bytes = (uint32_t)max(s_end, 0) * ROW;
     const rsrc_t krs = make_rsrc_uniform(a.k + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
     const rsrc_t vrs = make_rsrc_uniform(a.v + (size_t)kvh * (size_t)a.kv_stride * HD, kv_bytes);
-    uint8_t* vw = lds + wave * L::VT_WAVE;
+    int koff[L::NL], voff[L::NL];
+#pragma unroll
+    for (int j = 0; j < L::NL; ++j) {
+        const int b = 4096 * j + 16 * tid;
+        const int row = b / ROW, slot = (b % ROW) / 16;
+        koff[j] = row * ROW + 16 * rk_slot<HD>(row, slot);
+        voff[j] = row * ROW + 16 * rv_slot(row, slot);
+    }
+    // stage st into ring slot st % NSTAGE.  Stages past the split are issued too (they read
+    // zeros and touch no memory): every thread issues the same loads in the same order, so a
+    // fixed vmcnt tells when a stage has landed.
+    auto issue = [&](int st) {
+        const int sl = st % NSTAGE;
+        const int key0 = s_begin + L::SK * st;
+        lds_u8* kd = lds3 + sl * L::STAGE + 1024 * wave;
+        lds_u8* vd = lds3 + L::VBASE + sl * L::STAGE + 1024 * wave;
+#pragma unroll
+        for (int j = 0; j < L::NL; ++j) {
+            const int go = key0 * ROW + koff[j];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (void __attribute__((address_space(3)))*)(kd + 4096 * j), 16,
+                                                     go, 0, 0, kAuxNT);
+        }
+#pragma unroll
+        for (int j = 0; j < L::NL; ++j) {
+            const int go = key0 * ROW + voff[j];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (void __attribute__((address_space(3)))*)(vd + 4096 * j), 16,
+                                                     go, 0, 0, kAuxNT);
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < NSTAGE - 1; ++st) issue(st);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- Q conversion (waits for the Q loads only: they were issued before the ring)
+    vm_wait<(NSTAGE - 1) * L::LPS>();
+    f16x8 qh[KSW], ql[KSW];
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+        if constexpr (Q_F32) {
+            const f32x4 x0 = __builtin_bit_cast(f32x4, qraw[i][0]);
+            const f32x4 x1 = __builtin_bit_cast(f32x4, qraw[i][QV - 1]);
+            qh[i] = cvt_f16x8(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
+            ql[i] = cvt_f16x8(x0[0] - (float)qh[i][0], x0[1] - (float)qh[i][1], x0[2] - (float)qh[i][2],
+                              x0[3] - (float)qh[i][3], x1[0] - (float)qh[i][4], x1[1] - (float)qh[i][5],
+                              x1[2] - (float)qh[i][6], x1[3] - (float)qh[i][7]);
+        } else {
+            qh[i] = as_f16x8(qraw[i][0]);
+        }
+    }
+
+    // ---- per-lane LDS read offsets within a stage slot
+    // K operand of score tile t, k-step ks: row 8*(n/4) + 4t + n%4, chunk 4 ks + g
+    int ka_off[KSW][2];
+#pragma unroll
+    for (int i = 0; i < KSW; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            ka_off[i][t] = (8 * (n >> 2) + 4 * t + (n & 3)) * ROW + 16 * rk_slot<HD>(8 * (n >> 2) + (n & 3),
+                                                                                      4 * (dg + DG * i) + g);
+    // V^T of output tile dt: lane i = n of 16-lane group g addresses row 8g + i/4 (and 4 rows
+    // on), dims 16 dt + 4 (i%4) .. +3; the read hands lane n the keys of dim 16 dt + n
+    int vt_off[DTW];
+    {
+        const int vr = 8 * g + (n >> 2);
+#pragma unroll
+        for (int w = 0; w < DTW; ++w) {
+            const int dt = dg * DTW + w;
+            vt_off[w] = L::VBASE + vr * ROW + 16 * rv_slot(vr, 2 * dt + ((n & 3) >> 1)) + 8 * (n & 1);
+        }
+    }
+    // partial scores: this wave's slot, and those of its row tile's DG waves in order
+    lds_u8* xw = lds3 + L::XBASE + (wave * 2 * 64 + lane) * 16;
+    const lds_u8* xr = lds3 + L::XBASE + (rt * DG * 2 * 64 + lane) * 16;
+
+    f32x4 o[DTW];
+#pragma unroll
+    for (int w = 0; w < DTW; ++w) o[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = kNegBig, l = 0.f;
     const float fc = EXT ? 1.f : a.scale_log2;
     const float cap_c1 = a.softcap > 0.f ? 2.f * kLog2e / a.softcap : 0.f, cap_c2 = a.softcap * kLog2e;
+    constexpr int VR = DTW < 4 ? DTW : 4;                       // V^T tiles read ahead of the PV MFMAs
 
-    // per-lane K rows of the two 16-key tiles: tile t, row n -> key 8*(n/4) + 4t + n%4
-    const uint32_t krow0 = 8 * (n >> 2) + (n & 3);
-    // V^T write bases of this lane (block i adds 4096*i: its dim chunk is 8 further)
-    int vt_wbase[4];
-    {
-        const int kq = lane & 7, cc0 = lane >> 3;
-#pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) vt_wbase[k2] = 512 * cc0 + 16 * ((kq >> 1) ^ k2) + 8 * (kq & 1);
-    }
+    for (int s = 0; s < n_st; ++s) {
+        // stage s has landed in every thread's share once each thread's own loads have
+        // (NSTAGE - 2 later stages may still be in flight) and every wave passed the barrier
+        vm_wait<(NSTAGE - 2) * L::LPS>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // every wave has finished stage s - 1: its slot takes stage s + NSTAGE - 1
+        issue(s + NSTAGE - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const lds_u8* kb = lds3 + (s % NSTAGE) * L::STAGE;
+        const int key0 = s_begin + L::SK * s;
 
-    constexpr int DEPTH = L::DEPTH;
-    u32x4 kb[DEPTH][2 * KS];
-    u32x4 vb[DEPTH][VB][4];
-    auto key0_of = [&](int s) { return s_begin + L::KEYS * (wave + NW * s); };
-    // K and V of step s into register buffer B (loads past the split read as zero)
-    auto issue = [&](auto B, int s) {
-        constexpr int b = DEPTH == 2 ? decltype(B)::value : 0;
-        const uint32_t key0 = (uint32_t)key0_of(s);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                kb[b][t * KS + ks] = buf_load16_nt(krs, ((key0 + krow0 + 4 * t) * HD + 32 * ks + 8 * g) * 2);
-#pragma unroll
-        for (int i = 0; i < VB; ++i) {
-            const int blk = lane + 64 * i;
-            const int kq = blk & 7, cc = blk >> 3;
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                vb[b][i][r4] = buf_load16_nt(vrs, ((key0 + 4 * kq + r4) * HD + 8 * cc) * 2);
-        }
-    };
-
-    f32x4 o[RT][DT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m[RT], l[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        m[rt] = kNegBig;
-        l[rt] = 0.f;
-    }
-
-    // step s consumes register buffer B = s & 1 (buffer 0 at depth 1), then refills it with
-    // step s + DEPTH
-    auto step = [&](auto B, int s) {
-        constexpr int b = DEPTH == 2 ? decltype(B)::value : 0;
-        const int key0 = key0_of(s);
-        // S^T = K Q^T for the two 16-key tiles
-        f32x4 sc[2][RT];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) sc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const f16x8 qh = *(const f16x8*)qslot(rt, ks, 0);
-                f16x8 ql;
-                if constexpr (Q_F32) ql = *(const f16x8*)qslot(rt, ks, 1);
+        // this wave's share of S^T = K Q^T for the two 16-key tiles: k-steps dg, dg + DG, ...
+        // (high and residual parts of f32 queries in separate accumulators: four chains)
+        f32x4 sh[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 sl2[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        u32x4 kr[KSW][2];
+        static_for<0, KSW>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if (dg + DG * i < KS) {                             // wave-uniform
+                kr[i][0] = lds_b128(kb + ka_off[i][0]);
+                kr[i][1] = lds_b128(kb + ka_off[i][1]);
+            }
+        });
+        static_for<0, KSW>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if (dg + DG * i < KS) {
+                lgkm_wait<0>(kr[i][0]);
+                lgkm_wait<0>(kr[i][1]);
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    const f16x8 ka = as_f16x8(kb[b][t * KS + ks]);
-                    sc[t][rt] = mfma16x16x32(ka, qh, sc[t][rt]);
-                    if constexpr (Q_F32) sc[t][rt] = mfma16x16x32(ka, ql, sc[t][rt]);
+                    const f16x8 ka = as_f16x8(kr[i][t]);
+                    sh[t] = mfma16x16x32(ka, qh[i], sh[t]);
+                    if constexpr (Q_F32) sl2[t] = mfma16x16x32(ka, ql[i], sl2[t]);
                 }
             }
-        // V^T of this step -> LDS: block (key quad kq, dim chunk cc) becomes 8 rows of 4 keys.
-        // Row 8*cc + dd, chunk kq/2 lands at vt_off = 512*cc + 64*dd + 16*((kq/2) ^ (dd/2)) +
-        // 8*(kq%2): four lane-dependent bases (one per dd/2) plus immediates.
+        });
+        f32x4 sp[2];
 #pragma unroll
-        for (int i = 0; i < VB; ++i) {
+        for (int t = 0; t < 2; ++t) sp[t] = Q_F32 ? sh[t] + sl2[t] : sh[t];
+        // hand the partial over, then read the row tile's partials once every wave wrote its own
+        *(__attribute__((address_space(3))) f32x4*)(xw) = sp[0];
+        *(__attribute__((address_space(3))) f32x4*)(xw + 1024) = sp[1];
+        // V^T operand reads of this wave's dims (they land during the exchange and softmax)
+        const lds_u8* vb = lds3 + (s % NSTAGE) * L::STAGE;
+        u32x2 va[VR][2];
+        static_for<0, VR>([&](auto W) {
+            constexpr int w = decltype(W)::value;
+            va[w][0] = lds_tr16<0>(vb + vt_off[w]);
+            va[w][1] = lds_tr16<4 * ROW>(vb + vt_off[w]);
+        });
+        asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(2 * VR) : "memory");   // own partial written
+        __builtin_amdgcn_s_barrier();
+        // every partial of the row tile (the wave's own one too: all DG waves then add the same
+        // values in the same order, d = 0, 1, ..., and hold bit-identical scores)
+        u32x4 xp[DG][2];
 #pragma unroll
-            for (int dd = 0; dd < 8; ++dd) {
-                const int wj = dd >> 1;
-                const uint32_t sel = (dd & 1) ? kSelHi : kSelLo;
-                u32x2 val;
-                val[0] = perm_b32(vb[b][i][1][wj], vb[b][i][0][wj], sel);
-                val[1] = perm_b32(vb[b][i][3][wj], vb[b][i][2][wj], sel);
-                *(u32x2*)(vw + vt_wbase[dd >> 1] + 4096 * i + 64 * dd) = val;
+        for (int d = 0; d < DG; ++d)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) xp[d][t] = lds_b128(xr + (d * 2 + t) * 1024);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        f32x4 sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            asm volatile("" : "+v"(xp[0][t]));                  // the wait above precedes every use
+            sc[t] = __builtin_bit_cast(f32x4, xp[0][t]);
+#pragma unroll
+            for (int d = 1; d < DG; ++d) {
+                asm volatile("" : "+v"(xp[d][t]));
+                sc[t] += __builtin_bit_cast(f32x4, xp[d][t]);
             }
         }
-        // both register halves of this step are consumed: refill them with step s + DEPTH.  The
-        // loads are unconditional (steps past the split read as zero through the descriptor
-        // and touch no memory), so every iteration issues the same loads in the same order
-        // and the compiler's wait counts keep two steps in flight.
-        __builtin_amdgcn_sched_barrier(0);
-        issue(B, s + DEPTH);
-        __builtin_amdgcn_sched_barrier(0);
-        wave_lds_sync();
-        // mask, online softmax (log2 units)
-        f16x8 pb[RT];
+
+        // mask (only stages with a key some row must not see), online softmax (log2 units)
+        const bool full = __all(key0 + L::SK - 1 <= khi && key0 >= klo) && key0 + L::SK <= s_end;
+        float mx = -INFINITY;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            float mx = -INFINITY;
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i) {
+                float x = sc[t][i];
+                if constexpr (EXT) {
+                    x *= a.scale;
+                    x = a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e;
+                }
+                if (!full) {
                     const int key = key0 + 8 * g + 4 * t + i;
-                    float x = sc[t][rt][i];
-                    if constexpr (EXT) {
-                        x *= a.scale;
-                        x = a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e;
-                    }
-                    const bool vis = rok[rt] && key < s_end && key <= khi[rt] && key >= klo[rt];
-                    x = vis ? x : -INFINITY;
-                    sc[t][rt][i] = x;
-                    mx = fmaxf(mx, x);
+                    x = (key < s_end && key <= khi && key >= klo) ? x : -INFINITY;
                 }
-            mx = max_xor32(max_xor16(mx));
-            const float m_new = fmaxf(m[rt], mx * fc);
-            if (__any(m_new != m[rt])) {
-                const float corr = fast_exp2(m[rt] - m_new);
-                l[rt] *= corr;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) o[rt][dt] *= corr;
-                m[rt] = m_new;
+                sc[t][i] = x;
+                mx = fmaxf(mx, x);
             }
-            float p[8];
+        mx = max_xor32(max_xor16(mx));
+        const float m_new = fmaxf(m, mx * fc);
+        if (__any(m_new != m)) {
+            const float corr = fast_exp2(m - m_new);
+            l *= corr;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) p[4 * t + i] = fast_exp2(fmaf(sc[t][rt][i], fc, -m[rt]));
-            l[rt] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-            pb[rt] = cvt_f16x8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+            for (int w = 0; w < DTW; ++w) o[w] *= corr;
+            m = m_new;
         }
-        // O^T += V^T P^T
+        float p[8];
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const f16x8 va = *(const f16x8*)(vw + vt_off(16 * dt + n, g, 0));
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) o[rt][dt] = mfma16x16x32(va, pb[rt], o[rt][dt]);
-        }
-        wave_lds_sync();
-    };
+            for (int i = 0; i < 4; ++i) p[4 * t + i] = fast_exp2(fmaf(sc[t][i], fc, -m));
+        l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        const f16x8 pb = cvt_f16x8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
 
-    // Steps run in pairs (static buffer indices); an odd count gets one fully masked step.
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    // The prologue issues in the same order as the loop (K then V, step by step), so the
-    // wait counts at the loop header stay those of the steady state.
-    __builtin_amdgcn_sched_barrier(0);
-    issue(I0{}, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (DEPTH == 2) issue(I1{}, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    if (wave == 0) store_q();
-    __syncthreads();
-    for (int s = 0; s < n_my; s += 2) {
-        step(I0{}, s);
-        step(I1{}, s + 1);
+        // O^T += V^T P^T for this wave's dims, VR tiles read ahead
+        static_for<0, DTW>([&](auto W) {
+            constexpr int w = decltype(W)::value;
+            constexpr int left = DTW - 1 - w < VR - 1 ? DTW - 1 - w : VR - 1;   // reads issued after w
+            lgkm_wait<2 * left>(va[w % VR][0], va[w % VR][1]);
+            const u32x4 vv = {va[w % VR][0][0], va[w % VR][0][1], va[w % VR][1][0], va[w % VR][1][1]};
+            o[w] = mfma16x16x32(as_f16x8(vv), pb, o[w]);
+            if constexpr (w + VR < DTW) {
+                va[w % VR][0] = lds_tr16<0>(vb + vt_off[w + VR]);
+                va[w % VR][1] = lds_tr16<4 * ROW>(vb + vt_off[w + VR]);
+            }
+        });
     }
+    // stages issued past the split are still landing in LDS: drain them before the
+    // workgroup's LDS can be handed to another workgroup
+    vm_wait<0>();
 
-    // ---- row sums across the four lanes of a row, then merge the NW waves in LDS (four
-    // waves: a tree, the upper half handing its (O, m, l) to the lower half, log2 NW times;
-    // eight: the flat merge below)
-    float lt[RT];
+    // ---- row sums across the four lanes of a row; lane (row n, group g) holds dims
+    // 16 dt + 4 g + (0..3) of row n
+    const float lt = sum_xor32(sum_xor16(l));
+    if (!rok) return;
+    const size_t prow = (size_t)qi * a.n_q_heads + h;
+    if (a.n_splits == 1) {
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        lt[rt] = sum_xor32(sum_xor16(l[rt]));
-    }
-    __syncthreads();                                       // V^T regions are reused below
-    auto put = [&](float* sl) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) sl[((rt * DT + dt) * 4 + i) * 64 + lane] = o[rt][dt][i];
-            sl[(L::OREGS + 2 * rt) * 64 + lane] = m[rt];
-            sl[(L::OREGS + 2 * rt + 1) * 64 + lane] = lt[rt];
-        }
-    };
-    auto take = [&](const float* sl) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const float m2 = sl[(L::OREGS + 2 * rt) * 64 + lane];
-            const float l2 = sl[(L::OREGS + 2 * rt + 1) * 64 + lane];
-            const float M = fmaxf(m[rt], m2);
-            const float c1 = fast_exp2(m[rt] - M), c2 = fast_exp2(m2 - M);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    o[rt][dt][i] = o[rt][dt][i] * c1 + sl[((rt * DT + dt) * 4 + i) * 64 + lane] * c2;
-            lt[rt] = lt[rt] * c1 + l2 * c2;
-            m[rt] = M;
-        }
-    };
-    if constexpr (L::FLAT_MERGE) {
-        // every wave hands its (O, m, l) over at once; wave w then folds the eight slots for
-        // the dim tiles dt = w, w + NW, ... (into o[rt][dt], with lt and m the merged row
-        // values) and writes those dims
-        put((float*)(lds + wave * L::MERGE_SLOT));
-        __syncthreads();
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            float ms[NW], M = -INFINITY;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                ms[w] = ((const float*)(lds + w * L::MERGE_SLOT))[(L::OREGS + 2 * rt) * 64 + lane];
-                M = fmaxf(M, ms[w]);
+        for (int w = 0; w < DTW; ++w) {
+            const int dim = 16 * (dg * DTW + w) + 4 * g;
+            const f32x4 y = o[w] * inv * gate4(a.gate, prow * HD + dim);
+            if constexpr (O_F32) {
+                *(f32x4*)((float*)a.out + prow * HD + dim) = y;
+            } else {
+                f32x2 p0 = {y[0], y[1]}, p1 = {y[2], y[3]};
+                f16x2 h0 = __builtin_convertvector(p0, f16x2);
+                f16x2 h1 = __builtin_convertvector(p1, f16x2);
+                u32x2 x = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
+                *(u32x2*)((uint16_t*)a.out + prow * HD + dim) = x;
             }
-            float Lt = 0.f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const float* sl = (const float*)(lds + w * L::MERGE_SLOT);
-                ms[w] = fast_exp2(ms[w] - M);                // the slot's weight
-                Lt += sl[(L::OREGS + 2 * rt + 1) * 64 + lane] * ms[w];
-            }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                if (dt % NW != wave) continue;               // wave-uniform
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    const float* sl = (const float*)(lds + w * L::MERGE_SLOT);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i] += sl[((rt * DT + dt) * 4 + i) * 64 + lane] * ms[w];
-                }
-                o[rt][dt] = acc;
-            }
-            lt[rt] = Lt;
-            m[rt] = M;
         }
     } else {
+        float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
 #pragma unroll
-        for (int half = NW / 2; half >= 1; half /= 2) {
-            if (wave >= half && wave < 2 * half) put((float*)(lds + (wave - half) * L::MERGE_SLOT));
-            __syncthreads();
-            if (wave < half) take((const float*)(lds + wave * L::MERGE_SLOT));
-            if (half > 1) __syncthreads();                 // slots are rewritten next level
+        for (int w = 0; w < DTW; ++w) {
+            const int dim = 16 * (dg * DTW + w) + 4 * g;
+            *(f32x2*)(pr + dim) = f32x2{o[w][0], o[w][1]};
+            *(f32x2*)(pr + dim + 2) = f32x2{o[w][2], o[w][3]};
         }
-        if (wave != 0) return;
-    }
-    // dim tiles this wave writes: all (tree merge: wave 0), or dt = wave, wave + NW, ... (flat)
-    auto mine = [&](int dt) { return !L::FLAT_MERGE || dt % NW == wave; };
-
-    // ---- lane (row n, group g) holds dims 16*dt + 4*g + (0..3) of its rows
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        if (!rok[rt]) continue;
-        const size_t prow = (size_t)qi[rt] * a.n_q_heads + h[rt];
-        if (a.n_splits == 1) {
-            const float inv = lt[rt] > 0.f ? 1.f / lt[rt] : 0.f;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                if (!mine(dt)) continue;
-                const int dim = 16 * dt + 4 * g;
-                const f32x4 y = o[rt][dt] * inv * gate4(a.gate, prow * HD + dim);
-                if constexpr (O_F32) {
-                    *(f32x4*)((float*)a.out + prow * HD + dim) = y;
-                } else {
-                    f32x2 p0 = {y[0], y[1]}, p1 = {y[2], y[3]};
-                    f16x2 h0 = __builtin_convertvector(p0, f16x2);
-                    f16x2 h1 = __builtin_convertvector(p1, f16x2);
-                    u32x2 x = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
-                    *(u32x2*)((uint16_t*)a.out + prow * HD + dim) = x;
-                }
-            }
-        } else {
-            float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                if (!mine(dt)) continue;
-                const int dim = 16 * dt + 4 * g;
-                *(f32x2*)(pr + dim) = f32x2{o[rt][dt][0], o[rt][dt][1]};
-                *(f32x2*)(pr + dim + 2) = f32x2{o[rt][dt][2], o[rt][dt][3]};
-            }
-            if (g == 0 && wave == 0) *(f32x2*)(pr + HD) = f32x2{m[rt] * kLn2, lt[rt]};   // m in natural-log units
-        }
+        if (g == 0 && dg == 0) *(f32x2*)(pr + HD) = f32x2{m * kLn2, lt};   // m in natural-log units
     }
 }
 
-// ---- LSE combine (qwen35_attn_comb.comp:16-40 without the gate):
+// ---- LSE combine (qwen35_attn_comb.comp:16-40, with the output gate of :34-38):
 // out[row][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, zeros for a row that
-// saw no key.  One workgroup per row: thread (split group sg, dim pair dp) folds splits
-// sg, sg + G, ... of dims 2dp, 2dp+1.  All of a thread's loads (its acc pairs and the
-// (m, l) pair every lane of a wave shares) are independent, so a batch of 16 splits is one
-// memory round trip; the G groups then merge through LDS.
-template <int HD>
-struct CombineLayout {
-    static constexpr int DP = HD / 2;                          // dim pairs per row
-    static constexpr int G = DP >= 256 ? 1 : 256 / DP;         // split groups
-    static constexpr int THREADS = DP * G;
-    static constexpr int BATCH = 16;                           // splits in flight per thread
-};
+// saw no key.  One workgroup per (row, 64 dims): thread (split group sg, dim quad dq) folds
+// splits sg, sg + 16, ... of dims 4 dq .. 4 dq + 3 of the slice, eight splits per memory
+// round trip (one round trip up to 128 splits); the 16 split groups merge through LDS.
+constexpr int kCombineSliceDims = 64;
+constexpr int kCombineSplitGroups = 16;
 
 template <int HD, bool O_F32>
-__global__ void __launch_bounds__(CombineLayout<HD>::THREADS)
-combine_kernel(CombineArgs a)
+__global__ void __launch_bounds__(256)
+combine_slices_kernel(CombineArgs a)
 {
-    using C = CombineLayout<HD>;
-    __shared__ float sm_m[C::G], sm_l[C::G];
-    __shared__ f32x2 sm_acc[C::G][C::DP];
+    constexpr int SG = kCombineSplitGroups, BATCH = 8;
+    __shared__ float sm_m[SG][16], sm_l[SG][16];
+    __shared__ f32x4 sm_acc[SG][16];
     const int row = blockIdx.x;
-    const int dp = threadIdx.x % C::DP, sg = threadIdx.x / C::DP;
+    const int dq = threadIdx.x & 15, sg = threadIdx.x >> 4;
+    const int dim = kCombineSliceDims * blockIdx.y + 4 * dq;
     const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
 
     float M = kNegBig * 4.f, L = 0.f;               // below any partial's m (kNegBig)
-    f32x2 acc = {0.f, 0.f};
-    for (int c0 = sg; c0 < a.n_splits; c0 += C::G * C::BATCH) {
-        f32x2 x[C::BATCH], ml[C::BATCH];
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = sg; c0 < a.n_splits; c0 += SG * BATCH) {
+        f32x2 x0[BATCH], x1[BATCH], ml[BATCH];
 #pragma unroll
-        for (int j = 0; j < C::BATCH; ++j) {
-            const int c = c0 + j * C::G;
+        for (int j = 0; j < BATCH; ++j) {
+            const int c = c0 + j * SG;
             const bool ok = c < a.n_splits;
             const float* ps = pr + (size_t)(ok ? c : 0) * (HD + 2);
-            x[j] = *(const f32x2*)(ps + 2 * dp);
+            x0[j] = *(const f32x2*)(ps + dim);
+            x1[j] = *(const f32x2*)(ps + dim + 2);
             ml[j] = *(const f32x2*)(ps + HD);
-            if (!ok) {
-                x[j] = f32x2{0.f, 0.f};
-                ml[j] = f32x2{kNegBig * 4.f, 0.f};
-            }
+            if (!ok) ml[j] = f32x2{kNegBig * 4.f, 0.f};
         }
         float Mb = M;
 #pragma unroll
-        for (int j = 0; j < C::BATCH; ++j) Mb = fmaxf(Mb, ml[j][0]);
+        for (int j = 0; j < BATCH; ++j) Mb = fmaxf(Mb, ml[j][0]);
         const float cr = fast_exp2((M - Mb) * kLog2e);
         acc *= cr;
         L *= cr;
 #pragma unroll
-        for (int j = 0; j < C::BATCH; ++j) {
-            const float w = fast_exp2((ml[j][0] - Mb) * kLog2e);
-            acc += x[j] * w;
+        for (int j = 0; j < BATCH; ++j) {
+            const float w = c0 + j * SG < a.n_splits ? fast_exp2((ml[j][0] - Mb) * kLog2e) : 0.f;
+            acc += f32x4{x0[j][0], x0[j][1], x1[j][0], x1[j][1]} * w;
             L += ml[j][1] * w;
         }
         M = Mb;
     }
-    if constexpr (C::G > 1) {
-        if (dp == 0) {
-            sm_m[sg] = M;
-            sm_l[sg] = L;
-        }
-        sm_acc[sg][dp] = acc;
-        __syncthreads();
-        if (sg != 0) return;
-        float Mt = sm_m[0];
+    sm_m[sg][dq] = M;
+    sm_l[sg][dq] = L;
+    sm_acc[sg][dq] = acc;
+    __syncthreads();
+    if (sg != 0) return;
+    float Mt = sm_m[0][dq];
 #pragma unroll
-        for (int j = 1; j < C::G; ++j) Mt = fmaxf(Mt, sm_m[j]);
-        acc = f32x2{0.f, 0.f};
-        L = 0.f;
+    for (int j = 1; j < SG; ++j) Mt = fmaxf(Mt, sm_m[j][dq]);
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    L = 0.f;
 #pragma unroll
-        for (int j = 0; j < C::G; ++j) {
-            const float w = fast_exp2((sm_m[j] - Mt) * kLog2e);
-            acc += sm_acc[j][dp] * w;
-            L += sm_l[j] * w;
-        }
+    for (int j = 0; j < SG; ++j) {
+        const float w = fast_exp2((sm_m[j][dq] - Mt) * kLog2e);
+        acc += sm_acc[j][dq] * w;
+        L += sm_l[j][dq] * w;
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    const f32x2 y = acc * inv * gate2(a.gate, (size_t)row * HD + 2 * dp);
+    const f32x4 y = acc * inv * gate4(a.gate, (size_t)row * HD + dim);
     if constexpr (O_F32) {
-        *(f32x2*)((float*)a.out + (size_t)row * HD + 2 * dp) = y;
+        *(f32x4*)((float*)a.out + (size_t)row * HD + dim) = y;
     } else {
-        const f16x2 hy = __builtin_convertvector(y, f16x2);
-        *(f16x2*)((_Float16*)a.out + (size_t)row * HD + 2 * dp) = hy;
+        f32x2 p0 = {y[0], y[1]}, p1 = {y[2], y[3]};
+        f16x2 h0 = __builtin_convertvector(p0, f16x2);
+        f16x2 h1 = __builtin_convertvector(p1, f16x2);
+        *(u32x2*)((uint16_t*)a.out + (size_t)row * HD + dim) =
+            u32x2{__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
     }
 }
 
 // The same merge for many rows with few splits (split prefill): one wave per row, four rows
 // per workgroup, lane l folding every split of dim pairs l, l + 64, ...; a batch of 8 splits
-// is one memory round trip.  The one-workgroup-per-row kernel above spends its time on
-// workgroup dispatch there (20480 rows x 2 splits: 37.8 us).
+// is one memory round trip.
 constexpr int kCombineRowsWaves = 4;
 
 template <int HD, bool O_F32>
@@ -604,7 +574,9 @@ static hipError_t launch_combine_t(const CombineArgs& a, hipStream_t stream)
         const int wgs = (a.n_rows + kCombineRowsWaves - 1) / kCombineRowsWaves;
         hipLaunchKernelGGL((combine_rows_kernel<HD, OF>), dim3(wgs), dim3(64 * kCombineRowsWaves), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((combine_kernel<HD, OF>), dim3(a.n_rows), dim3(CombineLayout<HD>::THREADS), 0, stream, a);
+        static_assert(HD % kCombineSliceDims == 0, "combine slices");
+        hipLaunchKernelGGL((combine_slices_kernel<HD, OF>), dim3(a.n_rows, HD / kCombineSliceDims), dim3(256), 0,
+                           stream, a);
     }
     return hipGetLastError();
 }
@@ -624,12 +596,12 @@ hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStr
 template <int HD, int RT, bool QF, bool OF, bool EXT>
 static hipError_t launch_decode_t(const DecodeArgs& a, int n_rowgroups, hipStream_t stream)
 {
-    constexpr int lds_bytes = DecodeLayout<HD, RT>::LDS_BYTES;
+    constexpr int lds_bytes = RingLayout<HD>::LDS_BYTES;
     static std::atomic<uint64_t> lds_set{0};          // devices whose LDS limit is raised
-    const hipError_t e = ensure_dyn_lds((const void*)decode_part_kernel<HD, RT, QF, OF, EXT>, lds_bytes, lds_set);
+    const hipError_t e = ensure_dyn_lds((const void*)decode_ring_kernel<HD, RT, QF, OF, EXT>, lds_bytes, lds_set);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((decode_part_kernel<HD, RT, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
-                       dim3(64 * DecodeLayout<HD, RT>::NW), lds_bytes, stream, a);
+    hipLaunchKernelGGL((decode_ring_kernel<HD, RT, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
+                       dim3(kDecodeThreads), lds_bytes, stream, a);
     return hipGetLastError();
 }
 
@@ -659,6 +631,7 @@ hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f
                          int n_rowgroups, hipStream_t stream)
 {
     if (a.row_tiles != 1 && a.row_tiles != 2) return hipErrorInvalidValue;
+    if (a.chunk % kDecodeKeys != 0 || a.chunk <= 0) return hipErrorInvalidValue;
     switch (head_dim) {
     case 64: return launch_decode_hd<64>(a, q_f32, o_f32, ext, n_rowgroups, stream);
     case 128: return launch_decode_hd<128>(a, q_f32, o_f32, ext, n_rowgroups, stream);

@@ -12,15 +12,13 @@ constexpr int kPrefillThreads = 256;
 // Pipelined prefill (attn_prefill_wide.hip): 32 query rows per wave, 4 waves per workgroup
 // as 4 row waves (KS = 1, 128 rows) or 2 row waves x 2 key groups (KS = 2, 64 rows).
 constexpr int kWideRowsPerWave = 32;
-// Split-KV decode: 4 waves per (split, kv head, row group), 32 keys per wave step,
-// 16 query rows (n_query * G) per row tile and one or two row tiles per row group.
+// Split-KV decode (attn_decode.hip): 4 waves per (split, kv head, row group) sharing an LDS
+// ring of 32-key stages, 16 query rows (n_query * G) per row tile and one or two row tiles
+// per row group.
 constexpr int kDecodeThreads = 256;
-// Waves per decode workgroup: 8 for head dims of 192 and 256, where one workgroup per CU
-// (the host's split rule there) then keeps two waves per SIMD streaming, and a workgroup's
-// fixed cost -- Q staging, the cross-wave merge, the partial -- is shared by twice the keys;
-// 4 below (two workgroups per CU).
-// (The host uses one row tile above head dim 128.)
-constexpr int decode_waves(int head_dim, int row_tiles) { return head_dim >= 192 && row_tiles == 1 ? 8 : 4; }
+// Decode workgroups resident per CU: two with a 64 KB ring up to head dim 128, one with a
+// 120-128 KB ring above.
+constexpr int decode_wg_per_cu(int head_dim) { return head_dim <= 128 ? 2 : 1; }
 constexpr int kDecodeKeys = 32;
 constexpr int kDecodeRowTile = 16;
 constexpr int kDecodeMaxRowTiles = 2;
@@ -56,7 +54,7 @@ struct DecodeArgs {
     int sliding_window;
     float scale, scale_log2, softcap;
     int n_splits;
-    int chunk;                      // keys per split, multiple of kDecodeKeys
+    int chunk;                      // keys per split, a positive multiple of kDecodeKeys
     int k_begin;                    // first key any row can see
     int k_end;                      // one past the last key any row can see
     int n_rows;                     // n_query * group
