@@ -26,11 +26,14 @@
 //    and V(s) while K(s+2) and V(s+1) load (buffer-load-to-LDS of XOR-swizzled 16-byte chunks,
 //    each lane choosing the global chunk for its LDS slot); one barrier per step.  With the loop unrolled by two
 //    the slot parity is static, so every LDS address is a per-lane register plus an immediate.
-//  * S^T = K Q^T with Q pre-scaled by scale * log2(e) and the accumulator seeded with -m, so a
-//    probability is one exp2; the running max moves lazily (only past a 2^8 margin), the row
-//    max is v_max3 + v_permlane32_swap, row sums are fp32 adds of the probabilities.  EXT:
-//    Q pre-scaled by scale, accumulators seeded with 0, and the VALU turns each raw score into
-//    softcap * tanh(x / softcap) * log2(e) - m (or x * log2(e) - m) before the row max.
+//  * S^T = K Q^T with Q as given -- f16 queries exactly, f32 queries as an f16 high part
+//    (registers) plus the f16 residual (LDS, a second MFMA per k-step), so scores carry ~22
+//    mantissa bits like the reference's f32 dot products -- and the accumulator seeded with
+//    -m (raw units), so a probability is exp2(scale * log2(e) * S): the scale is applied in
+//    f32, never folded into an f16 operand.  The running max moves lazily (only past a 2^8
+//    margin), the row max is v_max3 + v_permlane32_swap, row sums are fp32 adds of the
+//    probabilities.  EXT: accumulators seeded with 0, and the VALU turns each raw score into
+//    softcap * tanh(x scale / softcap) * log2(e) - m (or x scale log2(e) - m) before the row max.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -63,10 +66,15 @@ struct WideLayout {
     static constexpr int MERGE_FLOATS = NB * (HD / 32) * 16 * 64 + NB * 2 * 64;
     static constexpr int MERGE_BYTES = KS > 1 ? RWAVES * MERGE_FLOATS * 4 : 0;
     static constexpr int LDS_BYTES = RING_BYTES > MERGE_BYTES ? RING_BYTES : MERGE_BYTES;
+    // f32 queries: the f16 residual of each row wave's Q^T operands, [row wave][row block]
+    // [k-step][lane] x 16 bytes, after the ring (the merge reuses the ring once it is done)
+    static constexpr int QLO_WAVE = NB * (HD / 16) * 64 * 16;
+    static constexpr int QLO_BYTES = RWAVES * QLO_WAVE;
+    static constexpr int LDS_BYTES_QF32 = RING_BYTES + QLO_BYTES > MERGE_BYTES ? RING_BYTES + QLO_BYTES : MERGE_BYTES;
     static constexpr int LOADS = TILE / (kPrefillThreads * 16); // 16-byte loads per thread per tile
     static constexpr int SWZ = (CPR % 16 == 0) ? 15 : 7;
     static_assert(LOADS >= 1 && TILE % (kPrefillThreads * 16) == 0, "tile staging");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(LDS_BYTES_QF32 <= 160 * 1024, "LDS");
 };
 
 // Slot of global chunk c of K row r and of V row r (XOR swizzles that keep the operand reads
@@ -108,6 +116,16 @@ template <int N>
 __device__ __forceinline__ void wait_lgkm(u32x4& a)
 {
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm(u32x4& a, u32x4& b)
+{
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+// ds_write_b128 as inline asm (a plain LDS store makes the compiler drain the ring's loads)
+__device__ __forceinline__ void ds_write_b128(lds_u8* p, u32x4 v)
+{
+    asm volatile("ds_write_b128 %0, %1" : : "v"(p), "v"(v) : "memory");
 }
 
 // f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
@@ -153,6 +171,11 @@ __device__ __forceinline__ void mfma_s(f32x16& d, f16x8 a, const f16x8& b, const
 __device__ __forceinline__ void mfma_s_zero(f32x16& d, f16x8 a, const f16x8& b)
 {
     asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b));
+}
+//   S^T += A B, B (the f16 residual of f32 queries) in VGPRs
+__device__ __forceinline__ void mfma_s_lo(f32x16& d, f16x8 a, f16x8 b)
+{
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
 }
 template <int N1, int N2>
 __device__ __forceinline__ void acc_settle(f32x16 (&x)[N1][N2])
@@ -330,7 +353,10 @@ prefill_wide_kernel(PrefillArgs a)
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    static_assert(NB == 1 || !Q_F32, "the residual Q^T reads in the pipelined S phase assume one row block");
     f16x8 qt[NB][KSTEPS];
+    // this lane's 16 bytes of the row wave's residual Q^T operands (f32 queries)
+    const int qlo_lane = L::RING_BYTES + rw * L::QLO_WAVE + 16 * lane;
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
@@ -349,11 +375,20 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) x[i] = (float)hq[i];
             }
-            const float qs = EXT ? a.scale : a.scale_log2;      // softcap needs natural units
-            qt[rb][ks] = cvt_f16x8(x[0] * qs, x[1] * qs, x[2] * qs, x[3] * qs, x[4] * qs, x[5] * qs,
-                                   x[6] * qs, x[7] * qs);
+            // the query as given: the scale goes onto the scores in f32
+            qt[rb][ks] = cvt_f16x8(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+            if constexpr (Q_F32) {
+                // the f16 residual, one copy per row wave (key group 0 writes it); read by the
+                // second MFMA of each k-step
+                const f16x8 hq = qt[rb][ks];
+                const f16x8 lo = cvt_f16x8(x[0] - (float)hq[0], x[1] - (float)hq[1], x[2] - (float)hq[2],
+                                           x[3] - (float)hq[3], x[4] - (float)hq[4], x[5] - (float)hq[5],
+                                           x[6] - (float)hq[6], x[7] - (float)hq[7]);
+                if (kg == 0) ds_write_b128(lds3 + qlo_lane + (rb * KSTEPS + ks) * 1024, as_u32x4(lo));
+            }
             if constexpr (kAgpr) asm volatile("" : "+a"(qt[rb][ks]));    // its home: AGPRs
         }
+    if constexpr (Q_F32) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // before the prologue barrier
 
     // ---- per-lane LDS read offsets within a tile
     // K operand of block sb, k-step ks: row 32 sb + n, chunk 2 ks + hh
@@ -375,9 +410,13 @@ prefill_wide_kernel(PrefillArgs a)
         }
     }
 
-    // ---- online-softmax state per row block: running max m_used (log2 units of the
-    // pre-scaled score), its negated splat (seed of every S^T accumulator), `seen` (the row
-    // has had a visible key) and this lane's share of the row sum
+    // ---- online-softmax state per row block: running max m_used (units of the raw score
+    // q.k; log2 units with EXT), its negated splat (seed of every S^T accumulator), `seen`
+    // (the row has had a visible key) and this lane's share of the row sum.  cs turns a
+    // seeded accumulator into log2 units (applied where the row max is taken, so the tile is
+    // in log2 units from then on: p = exp2(S)); inv_cs turns a log2 step back into raw units.
+    const float cs = EXT ? 1.f : a.scale_log2;
+    const float inv_cs = EXT ? 1.f : 1.f / a.scale_log2;
     f32x16 o[NB][DBLK];
     f32x16 negm[NB];
     float m_used[NB], l_part[NB];
@@ -413,15 +452,26 @@ prefill_wide_kernel(PrefillArgs a)
         static_for<0, KSTEPS * SB>([&](auto I) {
             constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
             u32x4 ka = ds_read_b128<32 * sb * L::ROW>(lds3 + ka_off[ks]);
+            u32x4 ql[NB];
+            if constexpr (Q_F32)
+#pragma unroll
+                for (int rb = 0; rb < NB; ++rb) ql[rb] = ds_read_b128<0>(lds3 + qlo_lane + (rb * KSTEPS + ks) * 1024);
             wait_lgkm<0>(ka);
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
+                if constexpr (Q_F32) wait_lgkm<0>(ql[rb]);
                 if constexpr (kAgpr && ks == 0)
                     mfma_s_zero(sn[rb][sb], __builtin_bit_cast(f16x8, ka), qt[rb][ks]);   // m = 0 here
                 else if constexpr (kAgpr)
                     mfma_s<false>(sn[rb][sb], __builtin_bit_cast(f16x8, ka), qt[rb][ks], negm[rb]);
                 else
                     sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+                if constexpr (Q_F32) {
+                    if constexpr (kAgpr)
+                        mfma_s_lo(sn[rb][sb], __builtin_bit_cast(f16x8, ka), __builtin_bit_cast(f16x8, ql[rb]));
+                    else
+                        sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka), __builtin_bit_cast(f16x8, ql[rb]), sn[rb][sb]);
+                }
             }
         });
     };
@@ -467,9 +517,9 @@ prefill_wide_kernel(PrefillArgs a)
             if constexpr (kAgpr) acc_settle(o);
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
-                const float d = need[rb] ? mx[rb] : 0.f;
+                const float d = need[rb] ? mx[rb] : 0.f;      // log2 units
                 const float corr = fast_exp2(-d);
-                m_used[rb] += d;
+                m_used[rb] += d * inv_cs;
                 seen[rb] = seen[rb] || need[rb];
                 l_part[rb] *= corr;
 #pragma unroll
@@ -485,11 +535,12 @@ prefill_wide_kernel(PrefillArgs a)
             }
         }
     };
-    // EXT: the MFMAs leave raw scaled scores q.k * scale (accumulators seeded with 0); the VALU
+    // EXT: the MFMAs leave raw scores q.k (accumulators seeded with 0); the VALU scales and
     // softcaps them, converts to log2 units and subtracts the running max
     const float cap_c1 = EXT && a.softcap > 0.f ? 2.f * kLog2e / a.softcap : 0.f;
     const float cap_c2 = a.softcap * kLog2e;
     auto ext_score = [&](float x, int rb) {
+        x *= a.scale;
         return (a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e) - m_used[rb];
     };
     // finish tile t's scores: mask if needed, row max, rescale
@@ -529,11 +580,16 @@ prefill_wide_kernel(PrefillArgs a)
     // these reads), each MFMA slot carries 1/KITER of the P work.
     auto phase_a = [&](auto KPAR, const STile& sc, STile& sn, PTile& pw) {
         constexpr int kbase = decltype(KPAR)::value * SLOT_PAR;
-        constexpr int AHEAD = KITER < kWideKAhead ? KITER : kWideKAhead;
-        u32x4 ka[KITER];
+        // f32 queries read the residual operand beside each K operand (two reads per slot,
+        // fewer slots ahead to stay within two waves' registers)
+        constexpr int KAH = Q_F32 ? 2 : kWideKAhead;
+        constexpr int AHEAD = KITER < KAH ? KITER : KAH;
+        constexpr int RPS = Q_F32 ? 2 : 1;               // LDS reads per slot
+        u32x4 ka[KITER], qlr[KITER];
         auto rd = [&](auto I) {
             constexpr int i = decltype(I)::value, ks = i / SB, sb = i % SB;
             ka[i] = ds_read_b128<kbase + 32 * sb * L::ROW>(lds3 + ka_off[ks]);
+            if constexpr (Q_F32) qlr[i] = ds_read_b128<ks * 1024>(lds3 + qlo_lane);
         };
         static_for<0, AHEAD>(rd);
         static_for<0, KITER>([&](auto I) {
@@ -541,7 +597,10 @@ prefill_wide_kernel(PrefillArgs a)
             if constexpr (i + AHEAD < KITER) rd(std::integral_constant<int, i + AHEAD>{});
             // reads issued after read i: i + 1 .. min(i + AHEAD, KITER - 1)
             constexpr int LATER = (KITER - 1 - i) < AHEAD ? (KITER - 1 - i) : AHEAD;
-            wait_lgkm<LATER>(ka[i]);
+            if constexpr (Q_F32)
+                wait_lgkm<RPS * LATER>(ka[i], qlr[i]);
+            else
+                wait_lgkm<LATER>(ka[i]);
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
                 if constexpr (kAgpr && EXT && ks == 0)
@@ -550,6 +609,12 @@ prefill_wide_kernel(PrefillArgs a)
                     mfma_s<ks == 0>(sn[rb][sb], __builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], negm[rb]);
                 else
                     sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka[i]), qt[rb][ks], ks == 0 ? negm[rb] : sn[rb][sb]);
+                if constexpr (Q_F32) {
+                    if constexpr (kAgpr)
+                        mfma_s_lo(sn[rb][sb], __builtin_bit_cast(f16x8, ka[i]), __builtin_bit_cast(f16x8, qlr[i]));
+                    else
+                        sn[rb][sb] = mfma32x32x16(__builtin_bit_cast(f16x8, ka[i]), __builtin_bit_cast(f16x8, qlr[i]), sn[rb][sb]);
+                }
             }
 #pragma unroll
             for (int pr = i * PAIRS / KITER; pr < (i + 1) * PAIRS / KITER; ++pr) p_pair(sc, pw, 2 * pr);
@@ -641,6 +706,9 @@ prefill_wide_kernel(PrefillArgs a)
                 if constexpr (EXT) {
                     sx[rb][sb][v] = ext_score(sx[rb][sb][v], rb);
                     sx[rb][sb][v + 1] = ext_score(sx[rb][sb][v + 1], rb);
+                } else {
+                    sx[rb][sb][v] *= cs;                          // raw units -> log2 units
+                    sx[rb][sb][v + 1] *= cs;
                 }
                 mrun[rb] = __builtin_fmaxf(mrun[rb], __builtin_fmaxf(sx[rb][sb][v], sx[rb][sb][v + 1]));
             }
@@ -679,13 +747,12 @@ prefill_wide_kernel(PrefillArgs a)
                 s_tile(sA);
                 if constexpr (kAgpr) s_settle(sA);
             }
-            if constexpr (EXT)
 #pragma unroll
-                for (int rb = 0; rb < NB; ++rb)
+            for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
-                    for (int sb = 0; sb < SB; ++sb)
+                for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) sA[rb][sb][v] = ext_score(sA[rb][sb][v], rb);
+                    for (int v = 0; v < 16; ++v) sA[rb][sb][v] = EXT ? ext_score(sA[rb][sb][v], rb) : sA[rb][sb][v] * cs;
             float mx[NB];
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) mx[rb] = row_max(sA, rb);
@@ -729,7 +796,7 @@ prefill_wide_kernel(PrefillArgs a)
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb) {
         l_tot[rb] = sum_xor32(l_part[rb]);
-        m_out[rb] = seen[rb] ? m_used[rb] : -INFINITY;
+        m_out[rb] = seen[rb] ? m_used[rb] * cs : -INFINITY;              // log2 units
     }
 
     if constexpr (KS > 1) {
@@ -743,7 +810,7 @@ prefill_wide_kernel(PrefillArgs a)
                 for (int db = 0; db < DBLK; ++db)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) mrg[((rb * DBLK + db) * 16 + v) * 64 + lane] = o[rb][db][v];
-                mrg[NB * DBLK * 16 * 64 + (2 * rb) * 64 + lane] = seen[rb] ? m_used[rb] : -INFINITY;
+                mrg[NB * DBLK * 16 * 64 + (2 * rb) * 64 + lane] = m_out[rb];
                 mrg[NB * DBLK * 16 * 64 + (2 * rb + 1) * 64 + lane] = l_tot[rb];
             }
         }
@@ -753,7 +820,7 @@ prefill_wide_kernel(PrefillArgs a)
             for (int rb = 0; rb < NB; ++rb) {
                 const float m1 = mrg[NB * DBLK * 16 * 64 + (2 * rb) * 64 + lane];
                 const float l1 = mrg[NB * DBLK * 16 * 64 + (2 * rb + 1) * 64 + lane];
-                const float m0 = seen[rb] ? m_used[rb] : -INFINITY;
+                const float m0 = m_out[rb];
                 const float mn = fmaxf(m0, m1);
                 const float c0 = mn == -INFINITY ? 0.f : fast_exp2(m0 - mn);
                 const float c1 = mn == -INFINITY ? 0.f : fast_exp2(m1 - mn);
@@ -826,7 +893,7 @@ int prefill_wide_rows(int ks) { return (4 / ks) * kWideRowsPerWave; }
 template <int HD, int KS, bool QF, bool OF, bool EXT>
 static hipError_t launch_wide_t(const PrefillArgs& a, hipStream_t stream)
 {
-    constexpr int lds_bytes = WideLayout<HD, KS>::LDS_BYTES;
+    constexpr int lds_bytes = QF ? WideLayout<HD, KS>::LDS_BYTES_QF32 : WideLayout<HD, KS>::LDS_BYTES;
     static std::atomic<uint64_t> lds_set{0};          // devices whose LDS limit is raised
     const hipError_t e = ensure_dyn_lds((const void*)prefill_wide_kernel<HD, KS, QF, OF, EXT>, lds_bytes, lds_set);
     if (e != hipSuccess) return e;

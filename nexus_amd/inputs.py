@@ -59,12 +59,14 @@ def f16_to_f32(bits: np.ndarray) -> np.ndarray:
 
 def make_case(*, n_q_heads: int, n_kv_heads: int, head_dim: int, n_query: int, n_ctx: int,
               kv_stride: int | None = None, seed: int = 1234, q_f16: bool = False,
-              kv_round: str = "rne"):
-    """Q (f32 values, f16-exact when q_f16), K/V f16 bits [Hkv][kv_stride][hd].
+              kv_round: str = "rne", q_scale: float = 1.0):
+    """Q (f32 values, N(0, q_scale^2), f16-exact when q_f16), K/V f16 bits [Hkv][kv_stride][hd].
     Rows of K/V past n_ctx (stride padding) are filled with a large finite sentinel so a
     kernel that reads them produces visibly wrong results."""
     stride = n_ctx if kv_stride is None else kv_stride
     q = normal(seed, n_query * n_q_heads * head_dim).reshape(n_query, n_q_heads, head_dim)
+    if q_scale != 1.0:
+        q = (q * np.float32(q_scale)).astype(np.float32)
     if q_f16:
         q = q.astype(np.float16).astype(np.float32)
     k = np.full((n_kv_heads, stride, head_dim), 0x7BFF, dtype=np.uint16)   # 65504

@@ -97,6 +97,42 @@ def test_flash_matches_cpu_attention(hip, hq, hkv, hd, nq, base, sw, cap):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("q_std", [4.0, 8.0])
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,n_rows", [
+    (40, 8, 128, 512, 4096, 1536),       # cfg2's shape (sampled rows checked)
+    (16, 2, 256, 256, 1000, 0),          # head dim 256 (one wave per SIMD, AGPR operands)
+    (8, 2, 128, 150, 100, 0),            # 64-row blocks with two key groups
+    (12, 4, 192, 130, 40, 0),            # head dim 192
+    (8, 2, 64, 200, 300, 0),             # head dim 64
+])
+def test_flash_precision_at_large_query_magnitudes(hip, q_std, hq, hkv, hd, nq, base, n_rows):
+    """The engine hands attention_flash_gpu f32 queries (transformer.h:8478-8494, as
+    attn_batch_cpu takes them, :8653).  With queries of std 4 and 8 the softmax is sharp and
+    an f16 rounding of q (or of q * scale) alone moves the output past 2e-3; the kernels keep
+    f32 queries as an f16 high part plus its f16 residual."""
+    lib = shim()
+    assert lib.shim_ready() == 1
+    n_ctx = base + nq
+    print(f"[case] flash q_std={q_std} hq={hq} hkv={hkv} hd={hd} nq={nq} base={base}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=41,
+                        q_scale=q_std)
+    out = np.zeros(q.shape, np.float32)
+    assert lib.shim_attention_flash_gpu(q, out, hq, hkv, hd, n_ctx, nq, base, 0, 0.0, 0.0, k, v) == 1, \
+        lib.shim_last_decline()
+    if n_rows:
+        rng = np.random.default_rng(7)
+        total = nq * hq
+        rows = np.unique(np.concatenate([[0, total - 1], rng.choice(total, n_rows, replace=False)])).astype(np.int32)
+        ref = O.attn_batch_rows(q, k, v, rows, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base,
+                                n_threads=8).reshape(total, hd)[rows]
+        got = out.reshape(total, hd)[rows]
+    else:
+        ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8)
+        got = out
+    assert_close(got, ref, f"flash q_std={q_std} hq={hq} hd={hd} nq={nq} base={base}")
+
+
+@pytest.mark.gpu
 def test_batch_and_stream_match_flash(hip):
     lib = shim()
     hq, hkv, hd, nq, base = 10, 2, 128, 60, 200

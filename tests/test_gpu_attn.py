@@ -379,3 +379,40 @@ def test_decode_gated(hip, hq, hkv, hd, nq, base, n_ctx, splits, of16):
     sat = np.abs(gate) > 80
     np.testing.assert_array_equal(got[sat & (gate > 0)], plain[sat & (gate > 0)])
     assert not np.any(got[sat & (gate < 0)])
+
+
+# ------------------------------------------- query magnitudes beyond N(0, 1)
+
+@pytest.mark.parametrize("q_std", [4.0, 8.0])
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,qf16", [
+    (40, 8, 128, 512, 4096, True),     # cfg2's shape, f16 queries used exactly as given
+    (40, 8, 128, 512, 4096, False),    # cfg2's shape, f32 queries (f16 high part + residual)
+    (16, 2, 256, 300, 600, True),      # head dim 256, f16 queries
+    (8, 2, 128, 64, 3000, False),      # a short chunk in key splits (partials in raw units)
+])
+def test_prefill_precision_at_large_query_magnitudes(hip, q_std, hq, hkv, hd, nq, base, qf16):
+    """Sharp softmaxes (queries of std 4 and 8): the scale is applied to the scores in f32, so
+    f16 queries are not rounded a second time and f32 queries keep ~22 mantissa bits."""
+    n_ctx = base + nq
+    print(f"[case] prefill q_std={q_std} hq={hq} hkv={hkv} hd={hd} nq={nq} base={base} qf16={qf16}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=43,
+                        q_f16=qf16, q_scale=q_std)
+    got = run_prefill(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, q_f16=qf16)
+    rows = _sample_rows(nq, hq, 1024, 3)
+    ref = O.attn_batch_rows(q, k, v, rows, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8)
+    assert_close(got.reshape(nq * hq, hd)[rows], ref.reshape(nq * hq, hd)[rows],
+                 f"prefill q_std={q_std} hd={hd} qf16={qf16}")
+
+
+@pytest.mark.parametrize("q_std", [4.0, 8.0])
+@pytest.mark.parametrize("hq,hkv,hd,nq,base,splits", [
+    (40, 8, 128, 1, 20000, 64),        # decode
+    (16, 2, 256, 4, 8000, 0),          # MTP verify
+])
+def test_decode_precision_at_large_query_magnitudes(hip, q_std, hq, hkv, hd, nq, base, splits):
+    n_ctx = base + nq
+    print(f"[case] decode q_std={q_std} hq={hq} hkv={hkv} hd={hd} nq={nq} base={base}", flush=True)
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=44, q_scale=q_std)
+    got = run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits)
+    ref = O.attn_batch(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_threads=8)
+    assert_close(got, ref, f"decode q_std={q_std} hd={hd} nq={nq}")
