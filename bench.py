@@ -82,7 +82,8 @@ def warm_up(call, warmup: int, min_s: float = WARM_S) -> None:
     torch.cuda.synchronize()
 
 
-def measure(name: str, steps: int, warmup: int, graph: bool = False, rotate: bool = True) -> dict:
+def measure(name: str, steps: int, warmup: int, graph: bool = False, rotate: bool = True,
+            check: bool = False) -> dict:
     import torch
 
     from nexus_amd import capi
@@ -155,6 +156,10 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False, rotate: boo
         res.update(gbs=gbs, frac_hbm=gbs / HBM_PEAK_GBS, mbytes=work / 1e6, splits=splits)
     if c["kind"] == "prefill":
         res["splits"] = (ws_bytes // (c["nq"] * c["hq"] * (c["hd"] + 2) * 4)) if ws_bytes else 1
+    if check:
+        call(0)
+        torch.cuda.synchronize()
+        res["parity"] = parity(name, c, q, kvs[0][0], kvs[0][1], out)
     tag = " (1 K/V copy)" if c["kind"] != "prefill" and n_sets == 1 else ""
     log(f"[bench] {name}{tag}: {ms * 1e3:.1f} us/step  " +
         (f"{res['tflops']:.1f} TFLOP/s ({100 * res['frac_mfma']:.1f}% MFMA)" if unit == "flop"
@@ -281,16 +286,64 @@ def measured_traffic(name: str):
         return None
 
 
+def cpu_info() -> dict:
+    """The host's CPU: the model string, the logical CPUs the OS reports (nproc) and the ones
+    this process may run on (its affinity set, the share a container or job scheduler gives it)."""
+    model, ids = "unknown", {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "model name" and model == "unknown":
+                model = val.strip()
+            elif key in ("cpu family", "model", "stepping", "vendor_id") and key not in ids:
+                ids[key] = val.strip()
+            elif key == "flags" and "avx512" not in ids:
+                ids["avx512"] = "avx512f" in val.split()
+            if line.strip() == "":
+                break                                    # the first processor's block is enough
+    except OSError:
+        pass
+    if ids:
+        model = f"{model} (vendor {ids.get('vendor_id', '?')}, family {ids.get('cpu family', '?')}, " \
+                f"model {ids.get('model', '?')}, stepping {ids.get('stepping', '?')}, " \
+                f"avx512 {'yes' if ids.get('avx512') else 'no'})"
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"model": model, "nproc": os.cpu_count() or 1, "usable": usable}
+
+
+def _timed(fn, target_s: float) -> tuple[float, int]:
+    """Seconds per call of fn, repeated until about target_s have passed (at least once)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            return el / n, n
+
+
 def cpu_baseline(target_s: float = 10.0) -> dict:
-    """The reference's CPU prefill attention (attn_batch_cpu, restated in oracle/) timed on a
-    bounded sample of the cfg2 workload: single thread (the reference's threading) plus an
-    all-cores variant."""
+    """The reference's CPU attention, restated in oracle/ (the parity checker), timed on this
+    host on bounded samples of the BASELINE workloads:
+      * prefill (cfg2, the headline): attn_batch_cpu (transformer.h:8653-8685) on a uniform
+        sample of (query, head) rows -- single thread, as the reference runs it (:8666), and
+        over every usable core (rows in parallel);
+      * decode (cfg1, cfg4): forward_cached_scores (attention.h:1201-1259) for one token --
+        with the reference's threading (heads in parallel on a pool of every usable core,
+        :1255-1257) and on one thread."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as O
+    from nexus_amd import capi
     from nexus_amd.inputs import make_case
 
+    info = cpu_info()
+    cores = info["usable"]
     c = CONFIGS["cfg2"]
     q, k, v = make_case(n_q_heads=c["hq"], n_kv_heads=c["hkv"], head_dim=c["hd"], n_query=c["nq"],
                         n_ctx=c["n_ctx"], seed=2024, q_f16=True)
@@ -313,13 +366,55 @@ def cpu_baseline(target_s: float = 10.0) -> dict:
     n = int(min(n_rows_total, max(16, target_s / max(per_row, 1e-6))))
     rows = order[:n]
     t1 = run(rows, 1)
-    threads = min(16, os.cpu_count() or 1)
-    rows_mt = order[: min(n_rows_total, n * threads // 2)]
-    tm = run(rows_mt, threads)
-    try:
-        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except Exception:
-        cpu_model = "unknown"
+    rows_mt = order[: min(n_rows_total, max(16, int(target_s / 2 / max(per_row, 1e-6)) * cores))]
+    tm = run(rows_mt, cores)
+
+    # the other attn_batch_cpu workloads: cfg3 on a row sample (a full single-thread run takes
+    # most of an hour), cfg5 whole (64 rows)
+    prefill_more = {}
+    for name, n_sample in (("cfg3", 1024), ("cfg5", 0)):
+        d = CONFIGS[name]
+        pq, pk, pv = make_case(n_q_heads=d["hq"], n_kv_heads=d["hkv"], head_dim=d["hd"], n_query=d["nq"],
+                               n_ctx=d["n_ctx"], seed=9, q_f16=d["q"] == "f16")
+        tot = d["nq"] * d["hq"]
+        prow = (np.arange(tot) if n_sample == 0 else rng.choice(tot, n_sample, replace=False)).astype(np.int32)
+        keys = np.minimum(d["base"] + prow // d["hq"], d["n_ctx"] - 1) + 1
+        pfl = float(4.0 * d["hd"] * keys.sum())
+        res = {}
+        for label, threads in (("one_thread", 1), ("all_cores", cores)):
+            t0 = time.perf_counter()
+            O.attn_batch_rows(pq, pk, pv, prow, n_kv_heads=d["hkv"], n_ctx=d["n_ctx"], q_base_pos=d["base"],
+                              n_threads=threads)
+            sec = time.perf_counter() - t0
+            res[label] = {"value": pfl / sec / 1e12, "unit": "TFLOP/s", "threads": threads, "seconds": sec}
+        res["sample"] = f"{len(prow)} of {tot} (query, head) rows"
+        prefill_more[name] = res
+
+    # decode: the reference's own forward_cached_scores, compiled from its sources into
+    # oracle/_ref (kind "reference"); the C restatement (kind "port") where that build is absent
+    decode = {}
+    use_ref = O.ref_available()
+    for name in ("cfg1", "cfg4"):
+        d = CONFIGS[name]
+        dq, dk, dv = make_case(n_q_heads=d["hq"], n_kv_heads=d["hkv"], head_dim=d["hd"], n_query=1, n_ctx=d["n_ctx"],
+                               seed=7)
+        nbytes = capi.decode_bytes(d["hkv"], d["hd"], d["n_ctx"], d["hq"], 1)
+        res = {"kind": "reference" if use_ref else "port",
+               "code": "oracle/_ref: forward_cached_scores (attention.h:1201-1259) built from the reference's sources"
+                       if use_ref else "oracle/attn_oracle.c restating attention.h:1201-1259"}
+        for label, threads in (("reference_threads", cores), ("one_thread", 1)):
+            if use_ref:
+                probe = O.ref_time_cached_scores(dq[0], dk, dv, n_kv_heads=d["hkv"], pos=d["base"], n_threads=threads,
+                                                 reps=1)
+                reps = max(1, min(200, int(target_s / 8 / max(probe, 1e-6))))
+                sec = O.ref_time_cached_scores(dq[0], dk, dv, n_kv_heads=d["hkv"], pos=d["base"], n_threads=threads,
+                                               reps=reps)
+            else:
+                sec, reps = _timed(lambda: O.cached_scores(dq[0], dk, dv, n_kv_heads=d["hkv"], pos=d["base"],
+                                                          n_threads=threads), target_s / 8)
+            res[label] = {"value": nbytes / sec / 1e9, "unit": "GB/s", "us_per_token": sec * 1e6, "threads": threads,
+                          "calls": reps}
+        decode[name] = res
     return {
         "value": flops(rows) / t1 / 1e12,
         "unit": "TFLOP/s",
@@ -327,10 +422,47 @@ def cpu_baseline(target_s: float = 10.0) -> dict:
         "kind": "port",
         "sample": f"{n} of {n_rows_total} (query, head) rows of cfg2 drawn uniformly, single thread "
                   f"({t1:.1f} s), oracle/attn_oracle.c restating transformer.h:8653-8685",
-        "all_cores": {"value": flops(rows_mt) / tm / 1e12, "cores": threads, "rows": int(len(rows_mt)),
+        "all_cores": {"value": flops(rows_mt) / tm / 1e12, "cores": cores, "rows": int(len(rows_mt)),
                       "seconds": tm},
-        "cpu_model": cpu_model,
+        "prefill": prefill_more,
+        "decode": decode,
+        "cpu": info,
     }
+
+
+def parity(name: str, c: dict, q, k, v, out, n_rows: int = 256) -> dict:
+    """The checker: max-abs and rel-L2 of the timed kernels' output against the CPU oracle
+    (attn_batch_cpu, transformer.h:8653-8685) on the inputs the bench timed -- every row for
+    decode and verify, a uniform sample of (query, head) rows (first and last included) for
+    prefill."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    qn = q.float().cpu().numpy()
+    kn = k.cpu().numpy().view(np.uint16)
+    vn = v.cpu().numpy().view(np.uint16)
+    got = out.float().cpu().numpy()
+    total = c["nq"] * c["hq"]
+    kw = dict(n_kv_heads=c["hkv"], n_ctx=c["n_ctx"], q_base_pos=c["base"], sliding_window=c.get("sw", 0),
+              softcap=c.get("cap", 0.0), n_threads=min(16, os.cpu_count() or 1))
+    if c["kind"] == "prefill":
+        rng = np.random.default_rng(11)
+        rows = np.unique(np.concatenate([[0, total - 1], rng.choice(total, min(n_rows, total), replace=False)]))
+        rows = rows.astype(np.int32)
+        ref = O.attn_batch_rows(qn, kn, vn, rows, **kw)
+        g = got.reshape(total, -1)[rows]
+        r = ref.reshape(total, -1)[rows]
+    else:
+        rows = np.arange(total)
+        g, r = got.reshape(total, -1), O.attn_batch(qn, kn, vn, **kw).reshape(total, -1)
+    res = {"max_abs": float(O.max_abs(g, r)), "rel_l2": float(O.rel_l2(g, r)), "rows_checked": int(len(rows)),
+           "rows_total": int(total), "tolerance": {"max_abs": 2e-3, "rel_l2": 1e-3}}
+    res["ok"] = res["max_abs"] < 2e-3 and res["rel_l2"] < 1e-3
+    log(f"[bench] {name} parity: max_abs={res['max_abs']:.2e} rel_l2={res['rel_l2']:.2e} "
+        f"({res['rows_checked']} of {total} rows) {'ok' if res['ok'] else 'FAILED'}")
+    return res
 
 
 def main() -> int:
@@ -367,18 +499,18 @@ def main() -> int:
         measure(args.only, args.steps, args.warmup)
         return 0
 
-    extra = {"cfg3": measure("cfg3", max(5, args.steps // 5), max(args.warmup, 20))}
-    head = measure("cfg2", args.steps, args.warmup)
+    extra = {"cfg3": measure("cfg3", max(5, args.steps // 5), max(args.warmup, 20), check=True)}
+    head = measure("cfg2", args.steps, args.warmup, check=True)
     for name in ("cfg4", "cfg1", "cfg5"):
-        extra[name] = measure(name, args.steps, args.warmup)
+        extra[name] = measure(name, args.steps, args.warmup, check=True)
     extra["cfg1_graph"] = measure("cfg1", args.steps, args.warmup, graph=True)
     # the same decode calls with one K/V copy (resident in the 256 MB Infinity Cache)
     extra["cfg4_warm"] = measure("cfg4", args.steps, args.warmup, rotate=False)
     extra["cfg5_warm"] = measure("cfg5", args.steps, args.warmup, rotate=False)
-    extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup)
-    extra["q35c"] = measure("q35c", args.steps, args.warmup)
-    extra["cap2"] = measure("cap2", args.steps, args.warmup)
-    extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup)
+    extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup, check=True)
+    extra["q35c"] = measure("q35c", args.steps, args.warmup, check=True)
+    extra["cap2"] = measure("cap2", args.steps, args.warmup, check=True)
+    extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup, check=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
 
     cpu = None
@@ -411,6 +543,7 @@ def main() -> int:
                                "over two waves; one launch per call, timed with HIP events on its stream)",
                      "algorithmic_gflop_per_call": head["gflop"]},
         "cpu_baseline": cpu,
+        "parity": head.get("parity"),
         "extra": extra,
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }

@@ -16,6 +16,7 @@
 // Transformer::attn_batch_cpu (model/transformer.h:8653-8685) is NOT built: its header
 // pulls in the Vulkan backend and the prebuilt SPIR-V blob headers, so it is restated
 // in attn_oracle.c and pinned against forward_cached_scores row by row instead.
+#include <chrono>
 #include "model/attention.h"
 
 #include <cstdint>
@@ -52,6 +53,37 @@ int ref_forward_cached_scores(const float* q, float* out, const uint16_t* K, con
     AttentionLayer layer;
     layer.forward_cached_scores(q, out, kv, 0, pos, cfg);
     return 0;
+}
+
+// Seconds per call of forward_cached_scores (the CPU baseline of the decode configs): the cache
+// is filled once, untimed, then `reps` calls are timed back to back with the reference's own
+// threading (n_threads: heads in parallel on its shared pool, attention.h:1255-1257).  Returns
+// -1 when the cache cannot be filled.
+double ref_time_cached_scores(const float* q, float* out, const uint16_t* K, const uint16_t* V,
+                              long kv_stride, int n_q_heads, int n_kv_heads, int head_dim,
+                              int pos, float scale, float softcap, int n_threads, int reps)
+{
+    KVCache kv;
+    kv.init(1, n_kv_heads, head_dim);
+    for (int h = 0; h < n_kv_heads; ++h) {
+        const size_t off = (size_t)h * (size_t)kv_stride * head_dim;
+        if (!kv.write_raw(0, h, 0, pos + 1, K + off, V + off)) return -1.0;
+    }
+    kv.set_n_tokens(pos + 1);
+    AttentionConfig cfg;
+    cfg.n_heads = n_q_heads;
+    cfg.n_kv_heads = n_kv_heads;
+    cfg.head_dim = head_dim;
+    cfg.scale = scale;
+    cfg.n_threads = n_threads;
+    cfg.attn_softcap = softcap;
+    cfg.sliding_window = 0;
+    AttentionLayer layer;
+    layer.forward_cached_scores(q, out, kv, 0, pos, cfg);          // warm: pool threads, pages
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < reps; ++i) layer.forward_cached_scores(q, out, kv, 0, pos, cfg);
+    const auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double>(t1 - t0).count() / (reps > 0 ? reps : 1);
 }
 
 // KVCache::store of `n_tok` tokens (f32 [n_tok][n_kv_heads*head_dim] each for K and V)

@@ -76,6 +76,8 @@ def ref() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(REF_SO))
         lib.ref_forward_cached_scores.argtypes = [_f32p, _f32p, _u16p, _u16p, _l, _i, _i, _i, _i, _f, _f, _i]
         lib.ref_forward_cached_scores.restype = _i
+        lib.ref_time_cached_scores.argtypes = [_f32p, _f32p, _u16p, _u16p, _l, _i, _i, _i, _i, _f, _f, _i, _i]
+        lib.ref_time_cached_scores.restype = ctypes.c_double
         lib.ref_kv_store_pack.argtypes = [_f32p, _f32p, _i, _i, _i, _u16p, _u16p]
         lib.ref_kv_store_pack.restype = _i
         lib.ref_kv_capacity_after.argtypes = [_i, _i]
@@ -116,14 +118,15 @@ def attn_batch(q, k, v, *, n_kv_heads, n_ctx, q_base_pos, sliding_window=0, scal
     return out
 
 
-def attn_batch_rows(q, k, v, rows, *, n_kv_heads, n_ctx, q_base_pos, scale=0.0, n_threads=1):
+def attn_batch_rows(q, k, v, rows, *, n_kv_heads, n_ctx, q_base_pos, scale=0.0, sliding_window=0, softcap=0.0,
+                    n_threads=1):
     q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
     nq, hq, hd = q.shape
     sc = scale if scale > 0 else 1.0 / np.sqrt(hd)
     out = np.zeros_like(q)
     rows = _c(rows, np.int32)
     oracle().oracle_attn_batch_rows(q, k, v, out, hq, n_kv_heads, hd, n_ctx, k.shape[1], nq, q_base_pos,
-                                    0, sc, 0.0, rows, len(rows), n_threads)
+                                    sliding_window, sc, softcap, rows, len(rows), n_threads)
     return out
 
 
@@ -145,6 +148,17 @@ def ref_cached_scores(q, k, v, *, n_kv_heads, pos, scale=0.0, softcap=0.0, n_thr
                                          softcap, n_threads)
     assert rc == 0
     return out
+
+
+def ref_time_cached_scores(q, k, v, *, n_kv_heads, pos, n_threads, reps, scale=0.0, softcap=0.0):
+    """Seconds per call of the reference's own forward_cached_scores over a cache filled once."""
+    q, k, v = _c(q, np.float32), _c(k, np.uint16), _c(v, np.uint16)
+    hq, hd = q.shape
+    out = np.zeros_like(q)
+    sec = ref().ref_time_cached_scores(q, out, k, v, k.shape[1], hq, n_kv_heads, hd, pos, scale, softcap,
+                                       n_threads, reps)
+    assert sec > 0
+    return sec
 
 
 def split_partials(q, k, v, *, n_kv_heads, n_ctx, q_base_pos, n_chunks, chunk, scale=0.0):

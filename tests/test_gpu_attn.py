@@ -41,9 +41,10 @@ def run_prefill(q, k, v, *, hkv, n_ctx, q_base, q_f16=False, o_f16=False, sw=0, 
     return out.float().cpu().numpy()
 
 
-def run_decode(q, k, v, *, hkv, n_ctx, q_base, n_splits=0, sw=0, cap=0.0, ws=None, gate=None, o_f16=False):
+def run_decode(q, k, v, *, hkv, n_ctx, q_base, n_splits=0, sw=0, cap=0.0, ws=None, gate=None, o_f16=False,
+               scale=0.0):
     out = ops.attn_decode(dev(q), dev(k), dev(v), n_kv_heads=hkv, q_base_pos=q_base, n_ctx=n_ctx,
-                          n_splits=n_splits, sliding_window=sw, softcap=cap, partial_ws=ws,
+                          n_splits=n_splits, sliding_window=sw, softcap=cap, partial_ws=ws, scale=scale,
                           gate=None if gate is None else dev(gate),
                           out_dtype=torch.float16 if o_f16 else torch.float32)
     torch.cuda.synchronize()
@@ -226,12 +227,18 @@ def test_decode_vs_oracle(hip, hq, hkv, hd, nq, base, n_ctx, splits, extra):
         assert_close(got[0], dec, "decode vs forward_cached_scores restatement")
 
 
-@pytest.mark.parametrize("name", ["dec_a", "dec_b", "dec_d"])
-def test_decode_golden(hip, golden, name):
+@pytest.mark.parametrize("name", ["dec_a", "dec_b", "dec_c", "dec_d"])
+@pytest.mark.parametrize("splits", [1, 0])
+def test_decode_golden(hip, golden, name, splits):
+    """Fixtures written by the reference's own forward_cached_scores (attention.h:1201-1259,
+    tests/golden/make_golden.py), with their scale and softcap (dec_c: scale 0.1, softcap 30,
+    which the reference computes with its Pade tanh, attention.h:232-245)."""
     hq, hkv, hd, pos = (int(x) for x in golden[f"{name}_meta"])
+    scale, cap = (float(x) for x in golden[f"{name}_fmeta"])
     q = golden[f"{name}_q"][None]
-    got = run_decode(q, golden[f"{name}_k"], golden[f"{name}_v"], hkv=hkv, n_ctx=pos + 1, q_base=pos)
-    assert_close(got[0], golden[f"{name}_out"], f"golden {name}")
+    got = run_decode(q, golden[f"{name}_k"], golden[f"{name}_v"], hkv=hkv, n_ctx=pos + 1, q_base=pos,
+                     n_splits=splits, scale=scale, cap=cap)
+    assert_close(got[0], golden[f"{name}_out"], f"golden {name} scale={scale} softcap={cap} splits={splits}")
 
 
 def test_decode_sliding_window_and_softcap(hip):

@@ -298,6 +298,39 @@ def test_split_combine_equals_unsplit(chunk):
     assert O.max_abs(y, r) < 2e-6 and O.rel_l2(y, r) < 1e-5
 
 
+@pytest.mark.parametrize("nq,chunk", [(1, 37), (3, 64)])
+def test_split_partials_meaning_per_chunk(nq, chunk):
+    """Each partial is (acc, m, l) of its chunk alone, as qwen35_attn_part.comp:62-70 writes
+    it: m = the chunk's max scaled score (natural-log units), l = sum_k e^{s_k - m},
+    acc = sum_k e^{s_k - m} v_k over the chunk's visible keys -- checked in float64 numpy per
+    chunk, so a units or offset mistake shared by the partial and the combine is caught."""
+    hq, hkv, hd, base = 4, 2, 64, 250
+    n_ctx = base + nq
+    q, k, v = make_case(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, n_query=nq, n_ctx=n_ctx, seed=17)
+    n_chunks = (n_ctx + chunk - 1) // chunk
+    scale = 1.0 / np.sqrt(hd)
+    part = O.split_partials(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_chunks=n_chunks, chunk=chunk)
+    part = part.reshape(nq * hq, n_chunks, hd + 2)
+    kf = k.view(np.float16).astype(np.float64)
+    vf = v.view(np.float16).astype(np.float64)
+    for qi in range(nq):
+        last = min(base + qi, n_ctx - 1)
+        for h in range(hq):
+            kv = h * hkv // hq
+            s = (kf[kv, : last + 1] @ q[qi, h].astype(np.float64)) * scale
+            for c in range(n_chunks):
+                lo, hi = c * chunk, min((c + 1) * chunk, last + 1)
+                pr = part[qi * hq + h, c]
+                if lo >= hi:                       # no visible key: l = 0, acc = 0
+                    assert pr[hd + 1] == 0.0 and not np.any(pr[:hd])
+                    continue
+                m = s[lo:hi].max()
+                e = np.exp(s[lo:hi] - m)
+                assert abs(pr[hd] - m) < 1e-5 * max(1.0, abs(m)), (qi, h, c)
+                assert abs(pr[hd + 1] - e.sum()) < 1e-5 * e.sum()
+                np.testing.assert_allclose(pr[:hd], e @ vf[kv, lo:hi], rtol=1e-4, atol=1e-5)
+
+
 def test_split_partials_causal_drafts():
     """Speculative verify rows: drafts at q_base + i see keys <= q_base + i."""
     hq, hkv, hd, base, nq = 8, 1, 256, 500, 4
