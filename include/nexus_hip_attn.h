@@ -100,9 +100,10 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc);
  * and the attention core of q35_full_layer (part + comb, vulkan_backend.h:5462-5482).
  * Two launches on `stream`, like the reference's part + comb: every split writes its
  * partial, then the combine merges them (one split writes `out` directly).  partial_ws
- * must hold nexus_hip_attn_decode_ws_bytes() bytes: f32
- * [n_query * n_q_heads][n_splits][head_dim + 2] partials holding, per split,
- * (sum_k e^{s_k - m} v_k, m, l) exactly as qwen35_attn_part.comp:3 defines them.  It
+ * must hold nexus_hip_attn_decode_ws_bytes() bytes: f32 partials holding, per row
+ * (n_query * n_q_heads of them) and split, (sum_k e^{s_k - m} v_k, m, l) exactly as
+ * qwen35_attn_part.comp:3 defines them, stored as acc [n_splits][rows][head_dim] followed
+ * by (m, l) [n_splits][rows][2] (16-byte stores, a split's rows contiguous).  It
  * carries no state between calls; calls in flight at once must not share it.
  * n_splits <= 0 lets the library choose. */
 int nexus_hip_attn_decode(const nexus_attn_desc* desc,

@@ -199,6 +199,20 @@ def decode_ws_bytes(desc: AttnDesc, n_splits: int = 0) -> int:
     return int(load().nexus_hip_attn_decode_ws_bytes(ctypes.byref(desc), int(n_splits)))
 
 
+def unpack_partials(ws, n_rows: int, n_splits: int, head_dim: int):
+    """The split partials in a decode workspace (a flat float32 array) as
+    [n_rows][n_splits][head_dim + 2] = (acc, m, l) per row and split, the reference's
+    partial (qwen35_attn_part.comp:3).  The library stores acc as [split][row][head_dim]
+    followed by (m, l) as [split][row][2]."""
+    import numpy as np
+
+    ws = np.asarray(ws, dtype=np.float32).reshape(-1)
+    n_acc = n_splits * n_rows * head_dim
+    acc = ws[:n_acc].reshape(n_splits, n_rows, head_dim)
+    ml = ws[n_acc:n_acc + 2 * n_splits * n_rows].reshape(n_splits, n_rows, 2)
+    return np.concatenate([acc, ml], axis=2).transpose(1, 0, 2).copy()
+
+
 def decode_default_splits(desc: AttnDesc) -> int:
     return int(load().nexus_hip_attn_decode_default_splits(ctypes.byref(desc)))
 

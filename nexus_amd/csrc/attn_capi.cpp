@@ -221,6 +221,7 @@ int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, const flo
     c.part = ws;
     c.out = out;
     c.gate = gate;
+    c.gate_stride = d->head_dim;
     c.n_rows = d->n_query * d->n_q_heads;
     c.n_splits = n_splits;
     const hipError_t e = nxa::launch_combine(c, d->head_dim, d->o_dtype == NEXUS_DT_F32, stream);
@@ -244,6 +245,7 @@ int run_decode(const nexus_attn_desc* d, const void* q, const uint16_t* k, const
     a.v = v;
     a.out = out;
     a.gate = gate;
+    a.gate_stride = d->head_dim;
     a.part = ws;
     a.kv_stride = d->kv_row_stride;
     a.n_q_heads = d->n_q_heads;

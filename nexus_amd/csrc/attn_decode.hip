@@ -4,8 +4,8 @@
 // qwen35_attn_comb.comp, dispatched back to back at src/gpu/vulkan_backend.h:5462-5482):
 //  * decode_ring_kernel: one workgroup per (split, kv head, row group) streams its slice of
 //    the cache once and writes, for every query row, acc[hd] = sum_k e^{s_k - m} v_k,
-//    m (the split's max scaled score) and l = sum_k e^{s_k - m} to
-//    part[row][split][hd + 2] -- the reference's partial format (qwen35_attn_part.comp:3).
+//    m (the split's max scaled score) and l = sum_k e^{s_k - m} -- the reference's partial
+//    (qwen35_attn_part.comp:3), stored as acc [split][row][hd] and (m, l) [split][row].
 //    With one split it writes the normalised output directly.
 //  * combine_slices_kernel: out = sum_c acc_c e^{m_c - M} / sum_c l_c e^{m_c - M},
 //    M = max_c m_c (qwen35_attn_comb.comp:16-40), output gate included.
@@ -403,7 +403,7 @@ decode_ring_kernel(DecodeArgs a)
 #pragma unroll
         for (int w = 0; w < DTW; ++w) {
             const int dim = 16 * (dg * DTW + w) + 4 * g;
-            const f32x4 y = o[w] * inv * gate4(a.gate, prow * HD + dim);
+            const f32x4 y = o[w] * inv * gate4(a.gate, prow * a.gate_stride + dim);
             if constexpr (O_F32) {
                 *(f32x4*)((float*)a.out + prow * HD + dim) = y;
             } else {
@@ -415,14 +415,13 @@ decode_ring_kernel(DecodeArgs a)
             }
         }
     } else {
-        float* pr = a.part + (prow * a.n_splits + split) * (HD + 2);
+        // 16-byte stores; the rows of this workgroup's split are contiguous in the workspace
+        const long long n_all = (long long)a.n_query * a.n_q_heads;
+        float* pr = a.part + part_acc(split, (long long)prow, n_all, HD);
 #pragma unroll
-        for (int w = 0; w < DTW; ++w) {
-            const int dim = 16 * (dg * DTW + w) + 4 * g;
-            *(f32x2*)(pr + dim) = f32x2{o[w][0], o[w][1]};
-            *(f32x2*)(pr + dim + 2) = f32x2{o[w][2], o[w][3]};
-        }
-        if (g == 0 && dg == 0) *(f32x2*)(pr + HD) = f32x2{m * kLn2, lt};   // m in natural-log units
+        for (int w = 0; w < DTW; ++w) *(f32x4*)(pr + 16 * (dg * DTW + w) + 4 * g) = o[w];
+        if (g == 0 && dg == 0)                                              // m in natural-log units
+            *(f32x2*)(a.part + part_ml(split, (long long)prow, n_all, a.n_splits, HD)) = f32x2{m * kLn2, lt};
     }
 }
 
@@ -444,20 +443,19 @@ combine_slices_kernel(CombineArgs a)
     const int row = blockIdx.x;
     const int dq = threadIdx.x & 15, sg = threadIdx.x >> 4;
     const int dim = kCombineSliceDims * blockIdx.y + 4 * dq;
-    const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
 
     float M = kNegBig * 4.f, L = 0.f;               // below any partial's m (kNegBig)
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int c0 = sg; c0 < a.n_splits; c0 += SG * BATCH) {
-        f32x2 x0[BATCH], x1[BATCH], ml[BATCH];
+        f32x4 x[BATCH];
+        f32x2 ml[BATCH];
 #pragma unroll
         for (int j = 0; j < BATCH; ++j) {
             const int c = c0 + j * SG;
             const bool ok = c < a.n_splits;
-            const float* ps = pr + (size_t)(ok ? c : 0) * (HD + 2);
-            x0[j] = *(const f32x2*)(ps + dim);
-            x1[j] = *(const f32x2*)(ps + dim + 2);
-            ml[j] = *(const f32x2*)(ps + HD);
+            const int cs = ok ? c : 0;
+            x[j] = *(const f32x4*)(a.part + part_acc(cs, row, a.n_rows, HD) + dim);
+            ml[j] = *(const f32x2*)(a.part + part_ml(cs, row, a.n_rows, a.n_splits, HD));
             if (!ok) ml[j] = f32x2{kNegBig * 4.f, 0.f};
         }
         float Mb = M;
@@ -469,7 +467,7 @@ combine_slices_kernel(CombineArgs a)
 #pragma unroll
         for (int j = 0; j < BATCH; ++j) {
             const float w = c0 + j * SG < a.n_splits ? fast_exp2((ml[j][0] - Mb) * kLog2e) : 0.f;
-            acc += f32x4{x0[j][0], x0[j][1], x1[j][0], x1[j][1]} * w;
+            acc += x[j] * w;
             L += ml[j][1] * w;
         }
         M = Mb;
@@ -491,7 +489,7 @@ combine_slices_kernel(CombineArgs a)
         L += sm_l[j][dq] * w;
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    const f32x4 y = acc * inv * gate4(a.gate, (size_t)row * HD + dim);
+    const f32x4 y = acc * inv * gate4(a.gate, (size_t)row * a.gate_stride + dim);
     if constexpr (O_F32) {
         *(f32x4*)((float*)a.out + (size_t)row * HD + dim) = y;
     } else {
@@ -516,7 +514,6 @@ combine_rows_kernel(CombineArgs a)
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * kCombineRowsWaves + (int)(threadIdx.x >> 6);
     if (row >= a.n_rows) return;
-    const float* pr = a.part + (size_t)row * a.n_splits * (HD + 2);
 
     float M = kNegBig * 4.f, L = 0.f;               // below any partial's m (kNegBig)
     f32x2 acc[PPL];
@@ -528,13 +525,13 @@ combine_rows_kernel(CombineArgs a)
         for (int j = 0; j < BATCH; ++j) {
             const int c = c0 + j;
             const bool ok = c < a.n_splits;
-            const float* ps = pr + (size_t)(ok ? c : 0) * (HD + 2);
+            const float* ps = a.part + part_acc(ok ? c : 0, row, a.n_rows, HD);
 #pragma unroll
             for (int p = 0; p < PPL; ++p) {
                 const int d = lane + 64 * p;
                 x[j][p] = (ok && d < DP) ? *(const f32x2*)(ps + 2 * d) : f32x2{0.f, 0.f};
             }
-            ml[j] = ok ? *(const f32x2*)(ps + HD) : f32x2{kNegBig * 4.f, 0.f};
+            ml[j] = ok ? *(const f32x2*)(a.part + part_ml(c, row, a.n_rows, a.n_splits, HD)) : f32x2{kNegBig * 4.f, 0.f};
         }
         float Mb = M;
 #pragma unroll
@@ -557,7 +554,7 @@ combine_rows_kernel(CombineArgs a)
     for (int p = 0; p < PPL; ++p) {
         const int d = lane + 64 * p;
         if (d >= DP) continue;
-        const f32x2 y = acc[p] * inv * gate2(a.gate, (size_t)row * HD + 2 * d);
+        const f32x2 y = acc[p] * inv * gate2(a.gate, (size_t)row * a.gate_stride + 2 * d);
         if constexpr (O_F32) {
             *(f32x2*)((float*)a.out + (size_t)row * HD + 2 * d) = y;
         } else {

@@ -30,7 +30,7 @@ struct PrefillArgs {
     const uint16_t* v;
     void* out;
     const float* gate;              // [n_query][Hq][hd] f32 or null: out *= sigmoid(gate)
-    float* part;                    // [n_query*Hq][n_splits][hd+2] partials (n_splits > 1)
+    float* part;                    // split partials of n_query*Hq rows (n_splits > 1), part_acc / part_ml
     long long kv_stride;            // tokens between kv heads
     int n_q_heads, n_kv_heads, group;
     int n_query, q_base, n_ctx;
@@ -46,8 +46,10 @@ struct DecodeArgs {
     const uint16_t* k;
     const uint16_t* v;
     void* out;                      // [n_query][Hq][hd]
-    const float* gate;              // [n_query][Hq][hd] f32 or null (applied with one split)
-    float* part;                    // [n_query*Hq][n_splits][hd+2] (n_splits > 1)
+    const float* gate;              // f32 gate of row qi*Hq + h at gate + row * gate_stride, or null
+                                    // (applied here with one split, by the combine otherwise)
+    long long gate_stride;          // floats between rows of the gate (hd, or 2 hd inside [q | gate])
+    float* part;                    // split partials of n_query*Hq rows (n_splits > 1), part_acc / part_ml
     long long kv_stride;
     int n_q_heads, n_kv_heads, group;
     int n_query, q_base, n_ctx;
@@ -62,9 +64,11 @@ struct DecodeArgs {
 };
 
 struct CombineArgs {
-    const float* part;              // [n_rows][n_splits][hd+2]
+    const float* part;              // split partials of n_rows rows, part_acc / part_ml
     void* out;                      // [n_rows][hd], row = qi*Hq + h
-    const float* gate;              // [n_rows][hd] f32 or null: out *= sigmoid(gate)
+    const float* gate;              // f32 gate of row r at gate + r * gate_stride, or null:
+                                    // out *= sigmoid(gate)
+    long long gate_stride;
     int n_rows, n_splits;
 };
 
@@ -96,11 +100,23 @@ struct PrepArgs {
     float eps;
 };
 
-// Workspace = f32 partials [rows][splits][hd+2], the reference's split-K partial format
-// (qwen35_attn_part.comp:3).  It carries no state between calls.
+// Workspace = f32 split partials with the meaning of the reference's split-K partials
+// (qwen35_attn_part.comp:3: per row and split, acc[hd] = sum_k e^{s_k - m} v_k, m, l), laid
+// out for 16-byte stores: acc as [split][row][hd], then (m, l) pairs as [split][row][2].  A
+// workgroup's rows of one split are contiguous, so its stores fill whole cache lines.  It
+// carries no state between calls.
 inline size_t ws_partial_bytes(long long rows, int splits, int head_dim)
 {
     return (size_t)rows * (size_t)splits * (size_t)(head_dim + 2) * sizeof(float);
+}
+// Offsets (in floats) of a partial's acc vector and of its (m, l) pair.
+__host__ __device__ inline size_t part_acc(int split, long long row, long long n_rows, int head_dim)
+{
+    return ((size_t)split * (size_t)n_rows + (size_t)row) * (size_t)head_dim;
+}
+__host__ __device__ inline size_t part_ml(int split, long long row, long long n_rows, int n_splits, int head_dim)
+{
+    return (size_t)n_splits * (size_t)n_rows * (size_t)head_dim + ((size_t)split * (size_t)n_rows + (size_t)row) * 2;
 }
 
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.

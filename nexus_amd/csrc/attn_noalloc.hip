@@ -17,7 +17,7 @@
 #include "capi_status.h"
 #include "nexus_hip_attn.h"
 
-// The partials of one call, f32 [n_query * n_q_heads][n_splits][head_dim + 2].
+// The split partials of one call (head_dim + 2 floats per row and split).
 constexpr size_t kScratchBytes = NEXUS_DECODE_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 

@@ -844,16 +844,17 @@ prefill_wide_kernel(PrefillArgs a)
         for (int rb = 0; rb < NB; ++rb) {
             const int qrow = w_first + 32 * rb + n;
             if (qrow >= a.n_query) continue;
-            float* pr = a.part + (((size_t)qrow * a.n_q_heads + h) * a.n_splits + split) * (HD + 2);
+            const long long prow = (long long)qrow * a.n_q_heads + h, n_all = (long long)a.n_query * a.n_q_heads;
+            float* pr = a.part + part_acc(split, prow, n_all, HD);
 #pragma unroll
             for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    const int dim = 32 * db + 8 * a4 + 4 * hh;
-                    *(f32x2*)(pr + dim) = f32x2{o[rb][db][4 * a4], o[rb][db][4 * a4 + 1]};
-                    *(f32x2*)(pr + dim + 2) = f32x2{o[rb][db][4 * a4 + 2], o[rb][db][4 * a4 + 3]};
-                }
-            if (hh == 0) *(f32x2*)(pr + HD) = f32x2{m_out[rb] > -INFINITY ? m_out[rb] * kLn2 : kNegBig, l_tot[rb]};
+                for (int a4 = 0; a4 < 4; ++a4)
+                    *(f32x4*)(pr + 32 * db + 8 * a4 + 4 * hh) =
+                        f32x4{o[rb][db][4 * a4], o[rb][db][4 * a4 + 1], o[rb][db][4 * a4 + 2], o[rb][db][4 * a4 + 3]};
+            if (hh == 0)
+                *(f32x2*)(a.part + part_ml(split, prow, n_all, a.n_splits, HD)) =
+                    f32x2{m_out[rb] > -INFINITY ? m_out[rb] * kLn2 : kNegBig, l_tot[rb]};
         }
         return;
     }

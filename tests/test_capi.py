@@ -127,7 +127,7 @@ def test_null_pointers_declined():
 
 
 def test_workspace_sizes():
-    # decode: f32 partials [n_query*Hq][n_splits][hd+2] and nothing else (no state)
+    # decode: f32 partials, (hd + 2) floats per row and split, and nothing else (no state)
     d = capi.make_desc(n_q_heads=40, n_kv_heads=8, head_dim=128, n_query=1, q_base_pos=61439, n_ctx=61440)
     assert capi.decode_ws_bytes(d, 64) == 40 * 64 * 130 * 4
     assert capi.decode_ws_bytes(d, 0) == 40 * capi.decode_default_splits(d) * 130 * 4

@@ -252,7 +252,7 @@ def test_decode_sliding_window_and_softcap(hip):
 
 
 def test_decode_partials_have_reference_meaning(hip):
-    """partial_ws[row][split] = (sum e^{s-m} v, m, l) over the split's keys, as
+    """The partial of every row and split is (sum e^{s-m} v, m, l) over the split's keys, as
     qwen35_attn_part.comp:3 defines them (m is the split's max score)."""
     hq, hkv, hd, base = 8, 2, 128, 1023
     n_ctx = base + 1
@@ -262,7 +262,7 @@ def test_decode_partials_have_reference_meaning(hip):
     ws = torch.zeros(capi.decode_ws_bytes(desc, splits) // 4, dtype=torch.float32, device="cuda")
     ws[: hq * splits * (hd + 2)] = float("nan")          # every partial must be written
     run_decode(q, k, v, hkv=hkv, n_ctx=n_ctx, q_base=base, n_splits=splits, ws=ws)
-    got = ws[: hq * splits * (hd + 2)].cpu().numpy().reshape(hq, splits, hd + 2)
+    got = capi.unpack_partials(ws.cpu().numpy(), hq, splits, hd)
     chunk = ((n_ctx + splits - 1) // splits + 31) // 32 * 32
     ref = O.split_partials(q, k, v, n_kv_heads=hkv, n_ctx=n_ctx, q_base_pos=base, n_chunks=splits, chunk=chunk)
     assert np.max(np.abs(got[:, :, hd] - ref[:, :, hd])) < 1e-4                     # m
