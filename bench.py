@@ -169,10 +169,11 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False, rotate: boo
 
 def measure_decode_layer(steps: int, warmup: int) -> dict:
     """The attention half of a gated full-attention decode layer over a device KV cache
-    (q35_full_layer's prep + part + comb): decode prep (q/k head norms, partial RoPE, f16
-    store of the new row) then gated split-KV decode, one token at 32768 cached tokens,
-    16 q / 2 kv heads, head_dim 256, RoPE over 64 dims.  The prep alone and the whole step
-    are timed with HIP events on the stream they run on."""
+    (q35_full_layer's prep + part + comb), one token at 32768 cached tokens, 16 q / 2 kv
+    heads, head_dim 256, RoPE over 64 dims: nexus_hip_attn_decode_layer (q/k head norms,
+    partial RoPE and the f16 store of the new row inside the split-KV kernel, then the gated
+    combine; two launches).  Beside it, the same step as prep kernel + gated decode (three
+    launches) and the prep alone.  Timed with HIP events on the stream the work runs on."""
     import torch
 
     from nexus_amd import capi, ops
@@ -214,11 +215,20 @@ def measure_decode_layer(steps: int, warmup: int) -> dict:
                              tab.data_ptr(), q_out.data_ptr(), gate.data_ptr(), k.data_ptr(), v.data_ptr(),
                              kvo.data_ptr(), stream)
 
-    def step(i, stream):
+    def two_step(i, stream):
         prep(i, stream)
         k, v = caches[i % n_sets]
         capi.decode_raw(desc, q_out.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr(), splits,
                         stream, gate=gate.data_ptr())
+
+    assert capi.decode_layer_default_splits(pdesc) == splits
+    assert capi.decode_layer_ws_bytes(pdesc, splits) <= ws.numel() * 4
+
+    def step(i, stream):
+        k, v = caches[i % n_sets]
+        capi.decode_layer_raw(pdesc, 0.0, qg.data_ptr(), kraw.data_ptr(), vraw.data_ptr(), qnw.data_ptr(),
+                              knw.data_ptr(), tab.data_ptr(), k.data_ptr(), v.data_ptr(), kvo.data_ptr(),
+                              out.data_ptr(), ws.data_ptr(), splits, stream)
 
     def timed(fn):
         stream = torch.cuda.current_stream(dev).cuda_stream
@@ -237,13 +247,16 @@ def measure_decode_layer(steps: int, warmup: int) -> dict:
         s1.synchronize()
         return s0.elapsed_time(s1) / steps
 
-    ms_prep, ms_step = timed(prep), timed(step)
+    ms_prep, ms_two, ms_step = timed(prep), timed(two_step), timed(step)
     kv_read = 2.0 * nkv * (pos + 1) * hd * 2
-    res = {"config": "decode_layer", "desc": "gated decode layer attention over a device KV cache: prep + "
-           "split-KV decode + gated combine, 1 token at 32768 cached tokens, 16q/2kv, hd256, rot 64",
-           "ms": ms_step, "prep_ms": ms_prep, "splits": splits, "kv_sets": n_sets, "launch": "graph",
+    res = {"config": "decode_layer", "desc": "gated decode layer attention over a device KV cache: "
+           "nexus_hip_attn_decode_layer (prep folded into the split-KV kernel, gated combine; two launches), "
+           "1 token at 32768 cached tokens, 16q/2kv, hd256, rot 64",
+           "ms": ms_step, "two_step_ms": ms_two, "prep_ms": ms_prep, "splits": splits, "kv_sets": n_sets,
+           "launch": "graph", "launches_per_step": 2,
            "gbs": kv_read / (ms_step * 1e-3) / 1e9, "frac_hbm": kv_read / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    log(f"[bench] decode_layer: {ms_step * 1e3:.1f} us/step (prep {ms_prep * 1e3:.1f} us)  "
+    log(f"[bench] decode_layer: {ms_step * 1e3:.1f} us/step fused (prep + decode as three launches "
+        f"{ms_two * 1e3:.1f} us, prep alone {ms_prep * 1e3:.1f} us)  "
         f"{res['gbs']:.0f} GB/s of K/V ({100 * res['frac_hbm']:.1f}% HBM)")
     return res
 

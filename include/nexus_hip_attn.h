@@ -198,6 +198,29 @@ int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* desc,
                                uint16_t* k_cache, uint16_t* v_cache, float* kv_out,
                                nexus_stream_t stream);
 
+/* The attention of one decode token of a full-attention layer, prep included: what
+ * nexus_hip_attn_decode_prep followed by nexus_hip_attn_decode_gated computes over
+ * k_cache / v_cache rows [0, pos] (row pos being the new token), in two launches instead of
+ * three.  Replaces the prep + part + comb dispatches of q35_full_layer
+ * (src/gpu/vulkan_backend.h:5446-5482).  The split-KV kernel normalises and rotates q in its
+ * prologue; the workgroups of the split that holds key `pos` prepare the new K/V row
+ * themselves, attend it, and store it into row `pos` of the caches and into kv_out, so no
+ * workgroup reads a row written in the same launch; the combine applies the gate, read from
+ * qg.  Arguments as for nexus_hip_attn_decode_prep (q_out / gate_out are not produced),
+ * plus the attention scale (0: 1/sqrt(head_dim)) and:
+ *   out        [n_heads][head_dim] f32: the gated attention output
+ *   partial_ws nexus_hip_attn_decode_layer_ws_bytes(desc, n_splits) bytes (split partials)
+ *   n_splits   <= 0 lets the library choose, as nexus_hip_attn_decode does.
+ * head_dim 64, 128, 192 or 256; the caches hold at least pos + 1 rows (cap > pos). */
+int nexus_hip_attn_decode_layer(const nexus_attn_prep_desc* desc, float scale,
+                                const float* qg, const float* k_raw, const float* v_raw,
+                                const float* q_norm_w, const float* k_norm_w, const float* rope_tab,
+                                uint16_t* k_cache, uint16_t* v_cache, float* kv_out, float* out,
+                                float* partial_ws, int n_splits, nexus_stream_t stream);
+size_t nexus_hip_attn_decode_layer_ws_bytes(const nexus_attn_prep_desc* desc, int n_splits);
+/* The split count nexus_hip_attn_decode_layer uses when called with n_splits <= 0. */
+int nexus_hip_attn_decode_layer_default_splits(const nexus_attn_prep_desc* desc);
+
 /* Message for the last non-zero status on the calling thread ("" if none). */
 const char* nexus_hip_attn_last_error(void);
 /* Library version, e.g. "nexus_hip_attn 0.1.0 gfx950". */

@@ -35,6 +35,9 @@ EXPORTED_SYMBOLS = (
     "nexus_hip_attn_decode_gated",
     "nexus_hip_attn_decode_prep",
     "nexus_hip_attn_decode_noalloc",
+    "nexus_hip_attn_decode_layer",
+    "nexus_hip_attn_decode_layer_ws_bytes",
+    "nexus_hip_attn_decode_layer_default_splits",
     "nexus_hip_kv_layer_bytes",
     "nexus_hip_kv_cache_bytes",
     "nexus_hip_kv_layer_save",
@@ -153,6 +156,13 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.nexus_hip_attn_decode_noalloc.restype = ctypes.c_int
     lib.nexus_hip_attn_decode_prep.argtypes = [ctypes.POINTER(PrepDesc)] + [vp] * 12
     lib.nexus_hip_attn_decode_prep.restype = ctypes.c_int
+    pdp = ctypes.POINTER(PrepDesc)
+    lib.nexus_hip_attn_decode_layer.argtypes = [pdp, ctypes.c_float] + [vp] * 11 + [ctypes.c_int, vp]
+    lib.nexus_hip_attn_decode_layer.restype = ctypes.c_int
+    lib.nexus_hip_attn_decode_layer_ws_bytes.argtypes = [pdp, ctypes.c_int]
+    lib.nexus_hip_attn_decode_layer_ws_bytes.restype = sz
+    lib.nexus_hip_attn_decode_layer_default_splits.argtypes = [pdp]
+    lib.nexus_hip_attn_decode_layer_default_splits.restype = ctypes.c_int
     kvp = ctypes.POINTER(KvLayerView)
     ip = ctypes.POINTER(ctypes.c_int)
     lib.nexus_hip_kv_layer_bytes.argtypes = [kvp, ctypes.c_int]
@@ -254,6 +264,23 @@ def decode_prep_raw(desc: PrepDesc, qg: int, k_raw: int, v_raw: int, q_norm_w: i
     rc = load().nexus_hip_attn_decode_prep(ctypes.byref(desc), qg, k_raw, v_raw, q_norm_w, k_norm_w, rope_tab,
                                            q_out, gate_out, k_cache, v_cache, kv_out, stream)
     return _check(rc) if check else rc
+
+
+def decode_layer_raw(desc: PrepDesc, scale: float, qg: int, k_raw: int, v_raw: int, q_norm_w: int, k_norm_w: int,
+                     rope_tab: int, k_cache: int, v_cache: int, kv_out: int, out: int, ws: int, n_splits: int,
+                     stream: int, check: bool = True) -> int:
+    """nexus_hip_attn_decode_layer: prep and gated split-KV decode of one token in two launches."""
+    rc = load().nexus_hip_attn_decode_layer(ctypes.byref(desc), float(scale), qg, k_raw, v_raw, q_norm_w, k_norm_w,
+                                            rope_tab, k_cache, v_cache, kv_out, out, ws, int(n_splits), stream)
+    return _check(rc) if check else rc
+
+
+def decode_layer_ws_bytes(desc: PrepDesc, n_splits: int = 0) -> int:
+    return int(load().nexus_hip_attn_decode_layer_ws_bytes(ctypes.byref(desc), int(n_splits)))
+
+
+def decode_layer_default_splits(desc: PrepDesc) -> int:
+    return int(load().nexus_hip_attn_decode_layer_default_splits(ctypes.byref(desc)))
 
 
 def prefill_flops(n_q_heads: int, head_dim: int, n_query: int, q_base_pos: int, n_ctx: int,

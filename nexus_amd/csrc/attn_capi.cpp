@@ -339,10 +339,14 @@ static_assert(NEXUS_PREP_Q_NORM_ADD_ONE == nxa::kPrepQZeroCentred && NEXUS_PREP_
                   NEXUS_PREP_TRUNC_STORE == nxa::kPrepTruncStore,
               "prep flag bits of the C ABI and the kernel differ");
 
-int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, const float* k_raw,
-                               const float* v_raw, const float* q_norm_w, const float* k_norm_w,
-                               const float* rope_tab, float* q_out, float* gate_out, uint16_t* k_cache,
-                               uint16_t* v_cache, float* kv_out, nexus_stream_t stream)
+}  // extern "C"
+
+namespace {
+
+// Descriptor and input checks shared by the prep and the fused decode layer.
+int check_prep(const nexus_attn_prep_desc* d, const float* qg, const float* k_raw, const float* v_raw,
+               const float* q_norm_w, const float* k_norm_w, const float* rope_tab, const uint16_t* k_cache,
+               const uint16_t* v_cache, const float* kv_out)
 {
     if (!d) return capi_fail(NEXUS_E_INVALID, "desc is NULL");
     if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->n_heads > 65536 || d->n_kv_heads > 65536)
@@ -356,13 +360,58 @@ int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, c
     if (d->flags & ~127) return capi_fail(NEXUS_E_INVALID, "unknown flag bits 0x%x", d->flags & ~127);
     if (!(d->eps >= 0.f) || !std::isfinite(d->eps)) return capi_fail(NEXUS_E_INVALID, "eps=%g", (double)d->eps);
     if (d->reserved != 0) return capi_fail(NEXUS_E_INVALID, "reserved=%d must be 0", d->reserved);
-    const bool gated = (d->flags & NEXUS_PREP_NO_GATE) == 0;
-    if (!qg || !k_raw || !v_raw || !q_out || !k_cache || !v_cache || !kv_out)
-        return capi_fail(NEXUS_E_INVALID, "null qg/k_raw/v_raw/q_out/k_cache/v_cache/kv_out pointer");
-    if (gated && !gate_out) return capi_fail(NEXUS_E_INVALID, "gate_out is NULL for a gated layer");
+    if (!qg || !k_raw || !v_raw || !k_cache || !v_cache || !kv_out)
+        return capi_fail(NEXUS_E_INVALID, "null qg/k_raw/v_raw/k_cache/v_cache/kv_out pointer");
     if (!(d->flags & NEXUS_PREP_NO_Q_NORM) && !q_norm_w) return capi_fail(NEXUS_E_INVALID, "q_norm_w is NULL");
     if (!(d->flags & NEXUS_PREP_NO_K_NORM) && !k_norm_w) return capi_fail(NEXUS_E_INVALID, "k_norm_w is NULL");
     if (d->rot_dims > 0 && !rope_tab) return capi_fail(NEXUS_E_INVALID, "rope_tab is NULL");
+    return NEXUS_OK;
+}
+
+// The attention descriptor of the fused decode layer: one token at pos over rows [0, pos]
+// of [n_kv][cap][hd] caches, f32 q and out.
+nexus_attn_desc layer_attn_desc(const nexus_attn_prep_desc* d, float scale)
+{
+    nexus_attn_desc a{};
+    a.n_q_heads = d->n_heads;
+    a.n_kv_heads = d->n_kv_heads;
+    a.head_dim = d->head_dim;
+    a.n_query = 1;
+    a.q_base_pos = d->pos;
+    a.n_ctx = d->pos + 1;
+    a.kv_row_stride = d->cap;
+    a.scale = scale;
+    a.q_dtype = NEXUS_DT_F32;
+    a.o_dtype = NEXUS_DT_F32;
+    return a;
+}
+
+// Shape checks of the fused layer beyond check_prep (decode head dims, a GQA group).
+int check_layer_shape(const nexus_attn_prep_desc* d, float scale)
+{
+    if (d->n_heads % d->n_kv_heads != 0)
+        return capi_fail(NEXUS_E_UNSUPPORTED, "n_heads=%d must be a multiple of n_kv_heads=%d", d->n_heads,
+                         d->n_kv_heads);
+    if (!supported_head_dim(d->head_dim))
+        return capi_fail(NEXUS_E_UNSUPPORTED, "head_dim=%d not in {64,128,192,256}", d->head_dim);
+    const nexus_attn_desc a = layer_attn_desc(d, scale);
+    return check_desc(&a);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, const float* k_raw,
+                               const float* v_raw, const float* q_norm_w, const float* k_norm_w,
+                               const float* rope_tab, float* q_out, float* gate_out, uint16_t* k_cache,
+                               uint16_t* v_cache, float* kv_out, nexus_stream_t stream)
+{
+    const int rc = check_prep(d, qg, k_raw, v_raw, q_norm_w, k_norm_w, rope_tab, k_cache, v_cache, kv_out);
+    if (rc != NEXUS_OK) return rc;
+    if (!q_out) return capi_fail(NEXUS_E_INVALID, "q_out is NULL");
+    const bool gated = (d->flags & NEXUS_PREP_NO_GATE) == 0;
+    if (gated && !gate_out) return capi_fail(NEXUS_E_INVALID, "gate_out is NULL for a gated layer");
 
     nxa::PrepArgs a{};
     a.qg = qg;
@@ -386,6 +435,96 @@ int nexus_hip_attn_decode_prep(const nexus_attn_prep_desc* d, const float* qg, c
     a.eps = d->eps;
     const hipError_t e = nxa::launch_decode_prep(a, (hipStream_t)stream);
     if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "decode prep launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+size_t nexus_hip_attn_decode_layer_ws_bytes(const nexus_attn_prep_desc* desc, int n_splits)
+{
+    if (!desc || check_layer_shape(desc, 0.f) != NEXUS_OK) return 0;
+    const nexus_attn_desc a = layer_attn_desc(desc, 0.f);
+    if (n_splits <= 0) n_splits = default_decode_splits(&a);
+    if (n_splits > kMaxSplits) return 0;
+    return decode_ws_bytes(&a, n_splits);
+}
+
+int nexus_hip_attn_decode_layer_default_splits(const nexus_attn_prep_desc* desc)
+{
+    if (!desc || check_layer_shape(desc, 0.f) != NEXUS_OK) return 0;
+    const nexus_attn_desc a = layer_attn_desc(desc, 0.f);
+    return default_decode_splits(&a);
+}
+
+int nexus_hip_attn_decode_layer(const nexus_attn_prep_desc* d, float scale, const float* qg, const float* k_raw,
+                                const float* v_raw, const float* q_norm_w, const float* k_norm_w,
+                                const float* rope_tab, uint16_t* k_cache, uint16_t* v_cache, float* kv_out,
+                                float* out, float* partial_ws, int n_splits, nexus_stream_t stream)
+{
+    int rc = check_prep(d, qg, k_raw, v_raw, q_norm_w, k_norm_w, rope_tab, k_cache, v_cache, kv_out);
+    if (rc != NEXUS_OK) return rc;
+    rc = check_layer_shape(d, scale);
+    if (rc != NEXUS_OK) return rc;
+    if (!out) return capi_fail(NEXUS_E_INVALID, "out is NULL");
+    const nexus_attn_desc ad = layer_attn_desc(d, scale);
+    if (n_splits > kMaxSplits) return capi_fail(NEXUS_E_UNSUPPORTED, "n_splits=%d > %d", n_splits, kMaxSplits);
+    if (n_splits <= 0) n_splits = default_decode_splits(&ad);
+    if (n_splits > 1 && !partial_ws) return capi_fail(NEXUS_E_WORKSPACE, "partial_ws is NULL");
+
+    int kb, ke;
+    key_range(&ad, &kb, &ke);
+    long long chunk = (ke - kb + n_splits - 1) / n_splits;
+    chunk = (chunk + nxa::kDecodeKeys - 1) / nxa::kDecodeKeys * nxa::kDecodeKeys;
+    if (chunk < nxa::kDecodeKeys) chunk = nxa::kDecodeKeys;
+    const bool gated = (d->flags & NEXUS_PREP_NO_GATE) == 0;
+    const int hd = d->head_dim;
+
+    nxa::DecodeArgs a{};
+    a.k = k_cache;
+    a.v = v_cache;
+    a.out = out;
+    a.gate = gated ? qg + hd : nullptr;
+    a.gate_stride = 2 * (long long)hd;
+    a.part = partial_ws;
+    a.kv_stride = d->cap;
+    a.n_q_heads = d->n_heads;
+    a.n_kv_heads = d->n_kv_heads;
+    a.group = d->n_heads / d->n_kv_heads;
+    a.n_query = 1;
+    a.q_base = d->pos;
+    a.n_ctx = d->pos + 1;
+    a.scale = eff_scale(&ad);
+    a.scale_log2 = a.scale * 1.4426950408889634f;
+    a.n_splits = n_splits;
+    a.chunk = (int)chunk;
+    a.k_begin = kb;
+    a.k_end = ke;
+    a.n_rows = (int)decode_rows(&ad);
+    a.row_tiles = decode_row_tiles(&ad);
+    a.qg = qg;
+    a.kraw = k_raw;
+    a.vraw = v_raw;
+    a.qnw = q_norm_w;
+    a.knw = k_norm_w;
+    a.tab = rope_tab;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.kv_out = kv_out;
+    a.rot = d->rot_dims;
+    a.prep_flags = d->flags;
+    a.pos_split = (int)((d->pos - kb) / chunk);
+    a.eps = d->eps;
+    const hipError_t e = nxa::launch_decode_layer(a, hd, decode_rowgroups(&ad), (hipStream_t)stream);
+    if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "decode layer launch: %s", hipGetErrorString(e));
+    if (n_splits > 1) {
+        nxa::CombineArgs c{};
+        c.part = partial_ws;
+        c.out = out;
+        c.gate = gated ? qg + hd : nullptr;
+        c.gate_stride = 2 * (long long)hd;
+        c.n_rows = d->n_heads;
+        c.n_splits = n_splits;
+        const hipError_t e2 = nxa::launch_combine(c, hd, true, (hipStream_t)stream);
+        if (e2 != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "combine launch: %s", hipGetErrorString(e2));
+    }
     return ok();
 }
 

@@ -145,6 +145,67 @@ __device__ __forceinline__ f32x2 gate2(const float* gate, size_t off)
     return f32x2{gate_sigmoid(z[0]), gate_sigmoid(z[1])};
 }
 
+// ---- decode prep math (one head on one 64-lane wave, lane l owning elements l, l + 64, ...),
+// shared by the prep kernel and the fused decode-layer kernel so both compute the same f32
+// values.  The norm is written as the host does it: cpu::rms_norm (src/cpu/matmul.h:1860-1880)
+// computes (x * w) * inv, nx_rms_norm_add_one (src/model/transformer.h:504-520) computes
+// x * inv * (1 + w), inv = 1 / sqrt(mean(x^2) + eps).  RoPE pairs are (i, i + rot/2)
+// (rotate_half) or (2i, 2i + 1) (interleaved), the two layouts of rope_apply
+// (src/model/attention.h:593-608), cos at tab[i] and sin at tab[rot/2 + i].
+__device__ __forceinline__ float prep_wave_sum(float x)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+__device__ __forceinline__ float prep_norm_inv(float sum_sq, int hd, float eps)
+{
+    return 1.0f / sqrtf(sum_sq / (float)hd + eps);
+}
+__device__ __forceinline__ float prep_norm_apply(float x, float inv, float w, bool add_one)
+{
+    return add_one ? x * inv * (1.0f + w) : (x * w) * inv;
+}
+// Rotated value of element d (< rot) from its own pre-rotation value x, its partner p
+// (prep_rope_partner) and the table entries c = tab[ci], s = tab[rot/2 + ci] with
+// ci = prep_rope_cos_index(d).
+__device__ __forceinline__ int prep_rope_partner(int d, int rot, bool interleaved)
+{
+    return interleaved ? (d ^ 1) : (d < (rot >> 1) ? d + (rot >> 1) : d - (rot >> 1));
+}
+__device__ __forceinline__ int prep_rope_cos_index(int d, int rot, bool interleaved)
+{
+    return interleaved ? (d >> 1) : (d < (rot >> 1) ? d : d - (rot >> 1));
+}
+__device__ __forceinline__ float prep_rope(int d, float x, float p, float c, float s, int rot, bool interleaved)
+{
+    if (interleaved) return (d & 1) == 0 ? x * c - p * s : p * s + x * c;
+    return d < (rot >> 1) ? x * c - p * s : x * c + p * s;
+}
+
+// f32 -> f16 bits, round to nearest even: the hardware conversion, which matches
+// KVCache::f32_to_f16_rne (src/model/kvcache.h:256-274) on every non-NaN input
+// (f16 subnormals are kept, overflow goes to inf); NaN becomes the quiet NaN that
+// function returns.
+__device__ __forceinline__ uint16_t f16_rne_bits(float f)
+{
+    if (f != f) return (uint16_t)(((__float_as_uint(f) >> 16) & 0x8000u) | 0x7e00u);
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// f32 -> f16 bits as KVCache::store converts (src/model/kvcache.h:903-911): mantissa
+// truncated, results below the f16 normal range flushed to signed zero, exponent
+// overflow (inf and NaN included) to signed inf.
+__device__ __forceinline__ uint16_t f16_trunc_bits(float f)
+{
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int e = (int)((x >> 23) & 0xffu) - 112;
+    if (e <= 0) return (uint16_t)sign;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)e << 10) | ((x >> 13) & 0x3ffu));
+}
+
 // Order this wave's LDS writes before its later LDS reads (wave-private LDS regions).
 __device__ __forceinline__ void wave_lds_sync()
 {

@@ -110,6 +110,31 @@ __device__ __forceinline__ void lgkm_wait(u32x2& a, u32x2& b)
 {
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
+// Scalar LDS accesses of the fused prep prologue, as inline asm for the same reason (the ring's
+// loads are in flight); waited for with lgkm_wait_all.
+__device__ __forceinline__ void lds_st32(lds_u8* p, float v)
+{
+    asm volatile("ds_write_b32 %0, %1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_st16(lds_u8* p, uint32_t v)
+{
+    asm volatile("ds_write_b16 %0, %1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_st128(lds_u8* p, u32x4 v)
+{
+    asm volatile("ds_write_b128 %0, %1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ float lds_ld32(const lds_u8* p)
+{
+    float r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ void lgkm_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// after lgkm_wait_all: the value is only used from here on
+__device__ __forceinline__ void after_wait(float& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void after_wait(u32x4& x) { asm volatile("" : "+v"(x)); }
+
 // s_waitcnt vmcnt(n) (expcnt and lgkmcnt left at their maxima)
 template <int N>
 __device__ __forceinline__ void vm_wait()
@@ -128,10 +153,11 @@ __device__ __forceinline__ void static_for(F&& f)
 
 }  // namespace
 
-template <int HD, int RT, bool Q_F32, bool O_F32, bool EXT>
+template <int HD, int RT, bool Q_F32, bool O_F32, bool EXT, bool PREP>
 __global__ void __launch_bounds__(kDecodeThreads, decode_wg_per_cu(HD))
 decode_ring_kernel(DecodeArgs a)
 {
+    static_assert(!PREP || (Q_F32 && O_F32 && !EXT), "the fused prep runs with f32 q and out, no softcap or window");
     using L = RingLayout<HD>;
     constexpr int KS = L::KS, ROW = L::ROW, NSTAGE = L::NSTAGE;
     constexpr int DG = 4 / RT;                                  // dim groups per row tile
@@ -167,7 +193,36 @@ decode_ring_kernel(DecodeArgs a)
     constexpr uint32_t QE = Q_F32 ? 4u : 2u;
     constexpr int QV = Q_F32 ? 2 : 1;
     u32x4 qraw[KSW][QV];
-    {
+    // PREP: the raw inputs of the prep go out before the ring, so converting them waits for
+    // them only.  Wave w prepares the q rows w, w + 4, ... of the workgroup (one head each,
+    // lane l owning elements l, l + 64, ... as decode_prep_kernel); in the workgroups of the
+    // split holding key pos, waves 0 and 1 also prepare the new K and V row.
+    constexpr int PER = HD / 64;
+    constexpr int PRW = PREP ? 4 * RT : 1;                      // q rows prepared per wave
+    float xq[PRW][PER], wq[PER], wk[PER], rc[PER], rs[PER], xn[PER];
+    const bool pos_wg = PREP && split == a.pos_split;           // workgroup-uniform
+    const bool gated = PREP && (a.prep_flags & kPrepNoGate) == 0;
+    const bool inter = (a.prep_flags & kPrepInterleaved) != 0;
+    if constexpr (PREP) {
+        const long long qstride = gated ? 2 * HD : HD;
+#pragma unroll
+        for (int i = 0; i < PRW; ++i) {
+            const int r = rg * (16 * RT) + wave + 4 * i;      // n_query = 1: row = head in group
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+                xq[i][j] = r < a.n_rows ? a.qg[(size_t)(kvh * a.group + r) * qstride + lane + 64 * j] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int d = lane + 64 * j;
+            wq[j] = (a.prep_flags & kPrepNoQNorm) ? 0.f : a.qnw[d];
+            const int ci = prep_rope_cos_index(d, a.rot, inter);
+            rc[j] = d < a.rot ? a.tab[ci] : 0.f;
+            rs[j] = d < a.rot ? a.tab[(a.rot >> 1) + ci] : 0.f;
+            wk[j] = pos_wg && wave == 0 && !(a.prep_flags & kPrepNoKNorm) ? a.knw[d] : 0.f;
+            xn[j] = pos_wg && wave < 2 ? (wave == 0 ? a.kraw : a.vraw)[(size_t)kvh * HD + d] : 0.f;
+        }
+    } else {
         const rsrc_t qr = make_rsrc_uniform(a.q, (uint32_t)((size_t)a.n_query * a.n_q_heads * HD * QE));
         // rows past n_rows point past the descriptor and read as zero
         const uint32_t qoff = rok ? (uint32_t)((((size_t)qi * a.n_q_heads + h) * HD + 8 * g) * QE) : 0x7fffff00u;
@@ -220,6 +275,95 @@ decode_ring_kernel(DecodeArgs a)
 
     // ---- Q conversion (waits for the Q loads only: they were issued before the ring)
     vm_wait<(NSTAGE - 1) * L::LPS>();
+    u32x4 kvchunk = {0u, 0u, 0u, 0u};    // PREP: wave 0 lane t holds 16 bytes of the new K|V row
+    if constexpr (PREP) {
+        // q rows go to the free ring slot NSTAGE - 1 (f32, rows 0-15 in its K half, 16-31 in its
+        // V half, 16-byte chunks XOR-swizzled by row); per-wave scratch for the RoPE partners
+        // and the new f16 K|V row go to the score-exchange area, unused until the first stage
+        auto qrow = [&](int r) {
+            return lds3 + (r < 16 ? 0 : L::VBASE) + (NSTAGE - 1) * L::STAGE + (r & 15) * (HD * 4);
+        };
+        auto qaddr = [&](int r, int d) { return qrow(r) + 16 * ((d >> 2) ^ (r & 15)) + 4 * (d & 3); };
+        lds_u8* scratch = lds3 + L::XBASE + wave * (HD * 4);
+        lds_u8* newrow = lds3 + L::XBASE + 4 * (HD * 4);       // [K | V] f16
+        // head norm (optional) and RoPE of one row held as x[j] = element lane + 64 j
+        auto prep_head = [&](float (&x)[PER], bool norm, bool add_one, const float (&w)[PER]) {
+            if (norm) {
+                float ss = 0.f;
+#pragma unroll
+                for (int j = 0; j < PER; ++j) ss += x[j] * x[j];
+                const float inv = prep_norm_inv(prep_wave_sum(ss), HD, a.eps);
+#pragma unroll
+                for (int j = 0; j < PER; ++j) x[j] = prep_norm_apply(x[j], inv, w[j], add_one);
+            }
+            if (a.rot > 0) {
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                    if (lane + 64 * j < a.rot) lds_st32(scratch + 4 * (lane + 64 * j), x[j]);
+                lgkm_wait_all();
+                float pr[PER];
+#pragma unroll
+                for (int j = 0; j < PER; ++j) {
+                    const int d = lane + 64 * j;
+                    pr[j] = lds_ld32(scratch + 4 * (d < a.rot ? prep_rope_partner(d, a.rot, inter) : 0));
+                }
+                lgkm_wait_all();
+#pragma unroll
+                for (int j = 0; j < PER; ++j) {
+                    after_wait(pr[j]);
+                    const int d = lane + 64 * j;
+                    if (d < a.rot) x[j] = prep_rope(d, x[j], pr[j], rc[j], rs[j], a.rot, inter);
+                }
+            }
+        };
+        const bool qnorm = (a.prep_flags & kPrepNoQNorm) == 0, qzc = (a.prep_flags & kPrepQZeroCentred) != 0;
+#pragma unroll
+        for (int i = 0; i < PRW; ++i) {
+            const int r = wave + 4 * i;
+            if (rg * (16 * RT) + r >= a.n_rows) continue;      // wave-uniform
+            prep_head(xq[i], qnorm, qzc, wq);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) lds_st32(qaddr(r, lane + 64 * j), xq[i][j]);
+        }
+        if (pos_wg && wave < 2) {
+            // the new row: K normed and rotated, V as given; stored as the cache stores it
+            if (wave == 0) prep_head(xn, (a.prep_flags & kPrepNoKNorm) == 0, (a.prep_flags & kPrepKZeroCentred) != 0, wk);
+            const bool trunc = (a.prep_flags & kPrepTruncStore) != 0;
+            uint16_t* dst = (wave == 0 ? a.kc : a.vc) + ((size_t)kvh * a.kv_stride + a.q_base) * HD;
+            float* echo = a.kv_out + ((size_t)wave * a.n_kv_heads + kvh) * HD;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int d = lane + 64 * j;
+                const uint16_t bits = trunc ? f16_trunc_bits(xn[j]) : f16_rne_bits(xn[j]);
+                if (rg == 0) {                                  // one row group stores it
+                    dst[d] = bits;
+                    echo[d] = xn[j];
+                }
+                lds_st16(newrow + 2 * (wave * HD + d), bits);
+            }
+        }
+        lgkm_wait_all();
+        __builtin_amdgcn_s_barrier();
+        // Q^T operands from the prepared rows (rows past n_rows compute with zeros)
+        const int rl = 16 * rt + n;
+#pragma unroll
+        for (int i = 0; i < KSW; ++i) {
+            const int ks = dg + DG * i;
+            if (ks < KS) {                                      // wave-uniform
+                qraw[i][0] = lds_b128(qaddr(rl, 32 * ks + 8 * g));
+                qraw[i][1] = lds_b128(qaddr(rl, 32 * ks + 8 * g + 4));
+            }
+        }
+        if (pos_wg && wave == 0 && lane < 2 * L::CPR) kvchunk = lds_b128(newrow + 16 * lane);
+        lgkm_wait_all();
+#pragma unroll
+        for (int i = 0; i < KSW; ++i) {
+            after_wait(qraw[i][0]);
+            after_wait(qraw[i][1]);
+            if (!rok || dg + DG * i >= KS) qraw[i][0] = qraw[i][1] = u32x4{0u, 0u, 0u, 0u};
+        }
+        after_wait(kvchunk);
+    }
     f16x8 qh[KSW], ql[KSW];
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
@@ -278,6 +422,18 @@ decode_ring_kernel(DecodeArgs a)
         __builtin_amdgcn_sched_barrier(0);
         const lds_u8* kb = lds3 + (s % NSTAGE) * L::STAGE;
         const int key0 = s_begin + L::SK * s;
+        if (PREP && pos_wg && a.q_base - key0 < L::SK) {        // workgroup-uniform: the stage of key pos
+            // the ring loaded row pos from the cache before this launch wrote it: replace it with
+            // the row prepared above (chunk c of K or V to the slot the ring loads put it in)
+            if (wave == 0 && lane < 2 * L::CPR) {
+                const int pr = a.q_base - key0, c = lane % L::CPR;
+                lds_u8* dst = lane < L::CPR ? lds3 + (s % NSTAGE) * L::STAGE + pr * ROW + 16 * rk_slot<HD>(pr, c)
+                                            : lds3 + L::VBASE + (s % NSTAGE) * L::STAGE + pr * ROW + 16 * rv_slot(pr, c);
+                lds_st128(dst, kvchunk);
+            }
+            lgkm_wait_all();
+            __builtin_amdgcn_s_barrier();
+        }
 
         // this wave's share of S^T = K Q^T for the two 16-key tiles: k-steps dg, dg + DG, ...
         // (high and residual parts of f32 queries in separate accumulators: four chains)
@@ -590,14 +746,15 @@ hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStr
     }
 }
 
-template <int HD, int RT, bool QF, bool OF, bool EXT>
+template <int HD, int RT, bool QF, bool OF, bool EXT, bool PREP = false>
 static hipError_t launch_decode_t(const DecodeArgs& a, int n_rowgroups, hipStream_t stream)
 {
     constexpr int lds_bytes = RingLayout<HD>::LDS_BYTES;
     static std::atomic<uint64_t> lds_set{0};          // devices whose LDS limit is raised
-    const hipError_t e = ensure_dyn_lds((const void*)decode_ring_kernel<HD, RT, QF, OF, EXT>, lds_bytes, lds_set);
+    const hipError_t e =
+        ensure_dyn_lds((const void*)decode_ring_kernel<HD, RT, QF, OF, EXT, PREP>, lds_bytes, lds_set);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((decode_ring_kernel<HD, RT, QF, OF, EXT>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
+    hipLaunchKernelGGL((decode_ring_kernel<HD, RT, QF, OF, EXT, PREP>), dim3(a.n_splits, a.n_kv_heads, n_rowgroups),
                        dim3(kDecodeThreads), lds_bytes, stream, a);
     return hipGetLastError();
 }
@@ -622,6 +779,26 @@ static hipError_t launch_decode_hd(const DecodeArgs& a, bool q_f32, bool o_f32, 
 {
     return a.row_tiles == 1 ? launch_decode_rt<HD, 1>(a, q_f32, o_f32, ext, nrg, s)
                             : launch_decode_rt<HD, 2>(a, q_f32, o_f32, ext, nrg, s);
+}
+
+template <int HD>
+static hipError_t launch_decode_layer_hd(const DecodeArgs& a, int nrg, hipStream_t s)
+{
+    return a.row_tiles == 1 ? launch_decode_t<HD, 1, true, true, false, true>(a, nrg, s)
+                            : launch_decode_t<HD, 2, true, true, false, true>(a, nrg, s);
+}
+
+hipError_t launch_decode_layer(const DecodeArgs& a, int head_dim, int n_rowgroups, hipStream_t stream)
+{
+    if (a.row_tiles != 1 && a.row_tiles != 2) return hipErrorInvalidValue;
+    if (a.chunk % kDecodeKeys != 0 || a.chunk <= 0 || a.n_query != 1) return hipErrorInvalidValue;
+    switch (head_dim) {
+    case 64: return launch_decode_layer_hd<64>(a, n_rowgroups, stream);
+    case 128: return launch_decode_layer_hd<128>(a, n_rowgroups, stream);
+    case 192: return launch_decode_layer_hd<192>(a, n_rowgroups, stream);
+    case 256: return launch_decode_layer_hd<256>(a, n_rowgroups, stream);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,

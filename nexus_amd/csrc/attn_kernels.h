@@ -61,6 +61,21 @@ struct DecodeArgs {
     int k_end;                      // one past the last key any row can see
     int n_rows;                     // n_query * group
     int row_tiles;                  // 16-row tiles per row group (1 or 2)
+    // Fused decode prep (the decode-layer kernel only; n_query = 1, f32 q and out): q is
+    // normalised and rotated from qg in the prologue, and the workgroups of the split holding
+    // key `pos` compute the new K/V row from kraw/vraw, attend it, and (row group 0) store it
+    // into kc/vc row `pos` and kv_out, as decode_prep_kernel does.
+    const float* qg;                // [Hq][2 hd] (q | gate) or [Hq][hd] with kPrepNoGate
+    const float* kraw;              // [Hkv][hd]
+    const float* vraw;
+    const float* qnw;               // [hd] or null (no q norm)
+    const float* knw;
+    const float* tab;               // [rot]: cos then sin
+    uint16_t* kc;                   // the cache a.k / a.v point into, written at row pos
+    uint16_t* vc;
+    float* kv_out;                  // [2][Hkv][hd]
+    int rot, prep_flags, pos_split;
+    float eps;
 };
 
 struct CombineArgs {
@@ -127,6 +142,9 @@ hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool 
                                hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, bool q_f32, bool o_f32, bool ext,
                          int n_rowgroups, hipStream_t stream);
+// The decode-layer form (prep fused, f32 q and out, n_query = 1): DecodeArgs with the prep
+// fields set.
+hipError_t launch_decode_layer(const DecodeArgs& a, int head_dim, int n_rowgroups, hipStream_t stream);
 hipError_t launch_combine(const CombineArgs& a, int head_dim, bool o_f32, hipStream_t stream);
 // Which combine kernel runs: one wave per row for many rows with few splits (split prefill),
 // one workgroup per row otherwise (decode: tens of rows, up to 256 splits).

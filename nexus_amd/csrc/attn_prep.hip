@@ -4,12 +4,8 @@
 //
 // Follows qwen35_attn_prep.comp:1-101 (flag bits, buffer layouts, workgroup -> head map):
 //   workgroups [0, n_heads) are q heads, [n_heads, n_heads + n_kv) k heads, then v heads.
-// The norm is written as the host does it, so the f32 results agree with the CPU path to
-// rounding: cpu::rms_norm (src/cpu/matmul.h:1860-1880) computes (x * w) * inv,
-// nx_rms_norm_add_one (src/model/transformer.h:504-520) computes x * inv * (1 + w), with
-// inv = 1 / sqrt(mean(x^2) + eps).  RoPE pairs are (i, i + rot/2) (rotate_half) or
-// (2i, 2i + 1) (interleaved), the two layouts of rope_apply (src/model/attention.h:593-608),
-// with cos at tab[i] and sin at tab[rot/2 + i].
+// The norm and RoPE follow the host code (prep_norm_apply / prep_rope in attn_common.h), so
+// the f32 results agree with the CPU path to rounding.
 //
 // MI355X shape: the whole op moves a few hundred KB, so it is launch-latency bound; one
 // 64-lane wave per head keeps every reduction inside the wave (no LDS tree, no barriers
@@ -23,36 +19,6 @@ namespace nxa {
 namespace {
 
 constexpr int kPrepPer = kPrepMaxHeadDim / 64;
-
-__device__ __forceinline__ float wave_sum(float x)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
-
-// f32 -> f16 bits, round to nearest even: the hardware conversion, which matches
-// KVCache::f32_to_f16_rne (src/model/kvcache.h:256-274) on every non-NaN input
-// (f16 subnormals are kept, overflow goes to inf); NaN becomes the quiet NaN that
-// function returns.
-__device__ __forceinline__ uint16_t f16_rne_bits(float f)
-{
-    if (f != f) return (uint16_t)(((__float_as_uint(f) >> 16) & 0x8000u) | 0x7e00u);
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
-// f32 -> f16 bits as KVCache::store converts (src/model/kvcache.h:903-911): mantissa
-// truncated, results below the f16 normal range flushed to signed zero, exponent
-// overflow (inf and NaN included) to signed inf.
-__device__ __forceinline__ uint16_t f16_trunc_bits(float f)
-{
-    const uint32_t x = __float_as_uint(f);
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    const int e = (int)((x >> 23) & 0xffu) - 112;
-    if (e <= 0) return (uint16_t)sign;
-    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
-    return (uint16_t)(sign | ((uint32_t)e << 10) | ((x >> 13) & 0x3ffu));
-}
 
 __global__ __launch_bounds__(64) void decode_prep_kernel(PrepArgs a)
 {
@@ -85,17 +51,16 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(PrepArgs a)
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < kPrepPer; ++j) ss += x[j] * x[j];
-            ss = wave_sum(ss);
-            const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+            const float inv = prep_norm_inv(prep_wave_sum(ss), hd, a.eps);
             const bool zc = (a.flags & (isq ? kPrepQZeroCentred : kPrepKZeroCentred)) != 0;
             const float* w = isq ? a.qnw : a.knw;
 #pragma unroll
             for (int j = 0; j < kPrepPer; ++j) {
                 const int d = lane + 64 * j;
-                if (d < hd) x[j] = zc ? x[j] * inv * (1.0f + w[d]) : (x[j] * w[d]) * inv;
+                if (d < hd) x[j] = prep_norm_apply(x[j], inv, w[d], zc);
             }
         }
-        const int rot = a.rot, half = rot >> 1;
+        const int rot = a.rot;
         if (rot > 0) {
 #pragma unroll
             for (int j = 0; j < kPrepPer; ++j) {
@@ -108,16 +73,9 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(PrepArgs a)
             for (int j = 0; j < kPrepPer; ++j) {
                 const int d = lane + 64 * j;
                 if (d >= rot) continue;
-                if (inter) {
-                    const int i = d >> 1;
-                    const float c = a.tab[i], s = a.tab[half + i];
-                    x[j] = (d & 1) == 0 ? row[d] * c - row[d + 1] * s : row[d - 1] * s + row[d] * c;
-                } else if (d < half) {
-                    x[j] = row[d] * a.tab[d] - row[d + half] * a.tab[half + d];
-                } else {
-                    const int i = d - half;
-                    x[j] = row[d] * a.tab[i] + row[i] * a.tab[half + i];
-                }
+                const int ci = prep_rope_cos_index(d, rot, inter);
+                x[j] = prep_rope(d, x[j], row[prep_rope_partner(d, rot, inter)], a.tab[ci], a.tab[(rot >> 1) + ci], rot,
+                                 inter);
             }
         }
     }

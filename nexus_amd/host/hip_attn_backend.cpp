@@ -55,12 +55,13 @@ HipAttnBackend::~HipAttnBackend()
     if (!ready_) return;
     (void)hipSetDevice(device_);
     (void)hipDeviceSynchronize();
-    for (DevBuf* b : {&q_, &k_, &v_, &o_, &ws_, &prep_q_, &prep_gate_, &prep_kv_, &prep_par_})
+    for (DevBuf* b : {&q_, &k_, &v_, &o_, &ws_, &prep_kv_, &prep_par_})
         if (b->ptr) (void)hipFree(b->ptr);
     for (auto& m : mirrors_) {
         if (m.second.k.ptr) (void)hipFree(m.second.k.ptr);
         if (m.second.v.ptr) (void)hipFree(m.second.v.ptr);
     }
+    if (chain_ring_) (void)hipHostFree(chain_ring_);
     if (ws_done_) (void)hipEventDestroy((hipEvent_t)ws_done_);
     if (stream_) (void)hipStreamDestroy((hipStream_t)stream_);
 }
@@ -380,14 +381,33 @@ bool HipAttnBackend::kv_mirror_read(const void* owner, int layer, int kv_head, i
     return true;
 }
 
+bool HipAttnBackend::chain_end()
+{
+    std::lock_guard<std::mutex> l(mu_);
+    if (!chain_open_) return true;
+    chain_open_ = false;
+    return hipStreamSynchronize((hipStream_t)chain_stream_) == hipSuccess;
+}
+
+const float* HipAttnBackend::chain_kv_ptr(int slot) const
+{
+    if (slot < 0 || slot >= kChainKvSlots || !chain_ring_) return nullptr;
+    return chain_ring_ + (size_t)slot * kChainSlotFloats;
+}
+
 bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const float* k_raw, const float* v_raw,
                                    float* attn_out, float* kv_out_host, uint32_t* mirror_valid_out,
-                                   nexus_stream_t stream)
+                                   nexus_stream_t stream, int async_kv_slot)
 {
     std::lock_guard<std::mutex> l(mu_);
     if (!ready_) return decline("no HIP device (HipAttnBackend::init not called or failed)");
-    if (!qg || !k_raw || !v_raw || !attn_out || !kv_out_host) return decline("q35_attention: null pointer");
+    const bool chained = async_kv_slot >= 0;
+    if (!qg || !k_raw || !v_raw || !attn_out || (!chained && !kv_out_host))
+        return decline("q35_attention: null pointer");
+    if (async_kv_slot >= kChainKvSlots) return decline("q35_attention: async_kv_slot >= kChainKvSlots");
     const uint32_t nh = d.n_heads, nkv = d.n_kv, hd = d.hd;
+    if (chained && (size_t)2 * nkv * hd > kChainSlotFloats)
+        return decline("q35_attention: K/V row larger than a chain slot (n_kv * hd > 8192)");
     if (nh == 0 || nkv == 0 || nh % nkv != 0) return decline("q35_attention: n_heads must be a multiple of n_kv");
     if (d.rot > hd || (d.rot & 1) || (d.rot > 0 && !d.rope_tab))
         return decline("q35_attention: rot must be even, <= hd, with a table");
@@ -418,6 +438,15 @@ bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const 
     if (cap_bytes == 0) return decline("q35_attention: GPU KV mirror is off (NEXUS_GPU_KV / set_gpu_kv_mb)");
     if (hipSetDevice(device_) != hipSuccess) return decline("hipSetDevice failed");
     hipStream_t s = stream ? (hipStream_t)stream : (hipStream_t)stream_;
+    if (chained) {
+        if (chain_open_ && chain_stream_ != (void*)s) return decline("q35_attention: chained calls on two streams");
+        if (!chain_ring_ && hipHostMalloc((void**)&chain_ring_, kChainKvSlots * kChainSlotFloats * sizeof(float),
+                                          hipHostMallocDefault) != hipSuccess) {
+            chain_ring_ = nullptr;
+            (void)hipGetLastError();
+            return decline("q35_attention: pinned allocation of the chain ring failed");
+        }
+    }
 
     // ---- find / grow (vulkan_backend.h:5349-5391)
     const std::pair<const void*, int> key{d.owner, d.layer};
@@ -489,10 +518,10 @@ bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const 
     KvMirror& m = it->second;
 
     // ---- per-call device buffers (grown, never shrunk)
-    const size_t q_bytes = (size_t)nh * hd * sizeof(float), kv_bytes = 2 * (size_t)nkv * hd * sizeof(float);
+    const size_t kv_bytes = 2 * (size_t)nkv * hd * sizeof(float);
     const size_t par_floats = (size_t)d.rot + 2 * (size_t)hd;
-    if (!ensure(prep_q_, q_bytes, false) || !ensure(prep_gate_, q_bytes, false) || !ensure(prep_kv_, kv_bytes, false) ||
-        !ensure(prep_par_, par_floats * sizeof(float), false) || !ensure(ws_, ws_bytes, true))
+    if (!ensure(prep_kv_, kv_bytes, false) || !ensure(prep_par_, par_floats * sizeof(float), false) ||
+        !ensure(ws_, ws_bytes, true))
         return decline("q35_attention: device scratch allocation failed");
 
     // ---- fill rows [eff_valid, pos) from the host (vulkan_backend.h:5392-5418)
@@ -523,7 +552,8 @@ bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const 
         (d.k_norm && hipMemcpyAsync(par + d.rot + hd, d.k_norm, hd * fb, hipMemcpyHostToDevice, s) != hipSuccess))
         return decline("q35_attention: parameter upload failed");
 
-    // ---- prep: head norms, RoPE, store of row `pos` (vulkan_backend.h:5446-5460)
+    // ---- prep + split-KV attention + gated combine (vulkan_backend.h:5446-5482) in two
+    // launches: the head norms, RoPE and the store of row `pos` run inside the split-KV kernel
     nexus_attn_prep_desc pd{};
     pd.n_heads = (int)nh;
     pd.n_kv_heads = (int)nkv;
@@ -536,27 +566,28 @@ bool HipAttnBackend::q35_attention(const KvLayerDesc& d, const float* qg, const 
                (d.has_gate ? 0 : NEXUS_PREP_NO_GATE) | (d.q_norm ? 0 : NEXUS_PREP_NO_Q_NORM) |
                (d.k_norm ? 0 : NEXUS_PREP_NO_K_NORM) | (d.rope_interleaved ? NEXUS_PREP_ROPE_INTERLEAVED : 0) |
                (mirror_rne_ ? 0 : NEXUS_PREP_TRUNC_STORE);
-    float* q_d = (float*)prep_q_.ptr;
-    float* gate_d = (float*)prep_gate_.ptr;
     float* kv_d = (float*)prep_kv_.ptr;
-    int rc = nexus_hip_attn_decode_prep(&pd, qg, k_raw, v_raw, d.q_norm ? qnw_d : nullptr, d.k_norm ? knw_d : nullptr,
-                                        d.rot ? tab_d : nullptr, q_d, d.has_gate ? gate_d : nullptr,
-                                        (uint16_t*)m.k.ptr, (uint16_t*)m.v.ptr, kv_d, (nexus_stream_t)s);
+    if (!ws_acquire(s)) return decline("hipStreamWaitEvent failed");
+    const int rc = nexus_hip_attn_decode_layer(&pd, d.scale, qg, k_raw, v_raw, d.q_norm ? qnw_d : nullptr,
+                                               d.k_norm ? knw_d : nullptr, d.rot ? tab_d : nullptr,
+                                               (uint16_t*)m.k.ptr, (uint16_t*)m.v.ptr, kv_d, attn_out,
+                                               (float*)ws_.ptr, splits, (nexus_stream_t)s);
+    ws_release(s);
     if (rc != NEXUS_OK) {
         m.valid = std::min<size_t>(m.valid, d.pos);
         return decline(nexus_hip_attn_last_error());
     }
-    // ---- split-KV attention over the mirror, output gate fused into the combine
-    ad.kv_row_stride = (int64_t)m.cap;
-    if (!ws_acquire(s)) return decline("hipStreamWaitEvent failed");
-    rc = nexus_hip_attn_decode_gated(&ad, q_d, (const uint16_t*)m.k.ptr, (const uint16_t*)m.v.ptr,
-                                     d.has_gate ? gate_d : nullptr, attn_out, (float*)ws_.ptr, splits,
-                                     (nexus_stream_t)s);
-    ws_release(s);
-    if (rc != NEXUS_OK) return decline(nexus_hip_attn_last_error());
-    if (hipMemcpyAsync(kv_out_host, kv_d, kv_bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
+    if (chained) {
+        // K/V into the ring slot; joined by chain_end()
+        if (hipMemcpyAsync(chain_ring_ + (size_t)async_kv_slot * kChainSlotFloats, kv_d, kv_bytes,
+                           hipMemcpyDeviceToHost, s) != hipSuccess)
+            return decline("q35_attention: device-to-host copy of K/V failed");
+        chain_open_ = true;
+        chain_stream_ = (void*)s;
+    } else if (hipMemcpyAsync(kv_out_host, kv_d, kv_bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+               hipStreamSynchronize(s) != hipSuccess) {
         return decline("q35_attention: device-to-host copy of K/V failed");
+    }
     m.valid = need;
     if (mirror_valid_out) *mirror_valid_out = need;
     ++calls_run_;

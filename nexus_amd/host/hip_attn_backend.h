@@ -101,8 +101,8 @@ public:
     // the attention part of VulkanBackend::q35_full_layer (src/gpu/vulkan_backend.h:
     // 5272-5483): the per-(owner, layer) mirror is found or grown, tokens the host changed
     // or the mirror never had are copied from the host cache (which stays the source of
-    // truth), then the prep kernel (head norms, RoPE, store of row `pos`) and the gated
-    // split-KV decode run over the mirror.  The projections before and the output
+    // truth), then nexus_hip_attn_decode_layer runs over the mirror: head norms, RoPE and the
+    // store of row `pos` inside the split-KV kernel, then the gated combine (two launches).  The projections before and the output
     // projection after stay with the caller: qg / k_raw / v_raw and attn_out are device
     // f32 buffers the engine's own matvecs produce and consume.
     struct KvLayerDesc {                                 // vulkan_backend.h:491-515, attention fields
@@ -127,9 +127,24 @@ public:
     // the value for KVCache::set_mirror_valid.  Declines (false, nothing touched) on an
     // unsupported shape, null pointers, host_tokens < pos, or when the mirror would
     // exceed the budget (then it also remembers the refused size, as the reference does).
+    //
+    // Chained form (the async_kv_slot of q35_full_layer, vulkan_backend.h:5275, joined by
+    // Transformer::q35_chain_flush, transformer.h:10083-10100): with async_kv_slot in
+    // [0, kChainKvSlots) the call returns once its work is queued; K then V of token `pos` land in
+    // slot async_kv_slot of a pinned host ring instead of kv_out_host (which may be null), and
+    // are read with chain_kv_ptr() after chain_end().  The device work of a call is the two
+    // launches of nexus_hip_attn_decode_layer plus the copies, so a chain of layers runs back to
+    // back on the stream; all chained calls use one stream.
     bool q35_attention(const KvLayerDesc& d, const float* qg, const float* k_raw, const float* v_raw,
                        float* attn_out, float* kv_out_host, uint32_t* mirror_valid_out,
-                       nexus_stream_t stream = nullptr);
+                       nexus_stream_t stream = nullptr, int async_kv_slot = -1);
+    static constexpr int kChainKvSlots = 16;
+    bool chain_is_open() const { return chain_open_; }
+    // Waits for every chained call (their attn_out and K/V slots are then complete); false when
+    // the stream reports an error.
+    bool chain_end();
+    // K/V of the chained call that used `slot` ([2][n_kv][hd] f32), valid after chain_end().
+    const float* chain_kv_ptr(int slot) const;
     // Free the mirrors of `owner`: one layer, or all of them when layer < 0
     // (vulkan_backend.h:5207-5217).
     void q35_kv_drop(const void* owner, int layer);
@@ -181,7 +196,12 @@ private:
     size_t kv_mirror_used_ = 0;
     int gpu_kv_mb_ = -2;                                 // -2: not read from the environment yet
     bool mirror_rne_ = false;
-    DevBuf prep_q_, prep_gate_, prep_kv_, prep_par_;
+    DevBuf prep_kv_, prep_par_;
+    // chained q35_attention: pinned K/V ring, kChainKvSlots slots of kChainSlotFloats
+    static constexpr size_t kChainSlotFloats = 2 * 16 * 512;   // 2 x n_kv <= 16 x hd <= 512
+    float* chain_ring_ = nullptr;
+    bool chain_open_ = false;
+    void* chain_stream_ = nullptr;
     bool ready_ = false;
     int device_ = -1;
     void* stream_ = nullptr;                 // hipStream_t

@@ -140,6 +140,24 @@ def decode_prep(qg: torch.Tensor, k_raw: torch.Tensor, v_raw: torch.Tensor, k_ca
     k_cache/v_cache [n_kv, cap, hd] (f16).  qg is [n_heads, 2*hd] (q | gate) when gated,
     else [n_heads, hd]; k_raw/v_raw [n_kv, hd]; all f32.  Returns (q_out [n_heads, hd],
     gate_out [n_heads, hd] or None, kv_out [2, n_kv, hd])."""
+    desc = _prep_desc(qg, k_raw, v_raw, k_cache, v_cache, pos=pos, rope_tab=rope_tab, q_norm_w=q_norm_w,
+                      k_norm_w=k_norm_w, gated=gated, q_norm_add_one=q_norm_add_one, k_norm_add_one=k_norm_add_one,
+                      rope_interleaved=rope_interleaved, eps=eps, trunc_store=trunc_store)
+    n_heads, n_kv, hd = desc.n_heads, desc.n_kv_heads, desc.head_dim
+    dev = qg.device
+    q_out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev) if q_out is None else q_out
+    if gated and gate_out is None:
+        gate_out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev)
+    kv_out = torch.empty(2, n_kv, hd, dtype=torch.float32, device=dev) if kv_out is None else kv_out
+    ptr = lambda t: 0 if t is None else t.data_ptr()
+    capi.decode_prep_raw(desc, qg.data_ptr(), k_raw.data_ptr(), v_raw.data_ptr(), ptr(q_norm_w), ptr(k_norm_w),
+                         ptr(rope_tab), q_out.data_ptr(), ptr(gate_out if gated else None), k_cache.data_ptr(),
+                         v_cache.data_ptr(), kv_out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+    return q_out, (gate_out if gated else None), kv_out
+
+
+def _prep_desc(qg, k_raw, v_raw, k_cache, v_cache, *, pos, rope_tab, q_norm_w, k_norm_w, gated, q_norm_add_one,
+               k_norm_add_one, rope_interleaved, eps, trunc_store):
     n_kv, cap, hd = k_cache.shape
     n_heads = qg.shape[0]
     f32 = [("qg", qg), ("k_raw", k_raw), ("v_raw", v_raw)]
@@ -160,17 +178,42 @@ def decode_prep(qg: torch.Tensor, k_raw: torch.Tensor, v_raw: torch.Tensor, k_ca
              | (capi.PREP_NO_K_NORM if k_norm_w is None else 0)
              | (capi.PREP_ROPE_INTERLEAVED if rope_interleaved else 0) | (capi.PREP_TRUNC_STORE if trunc_store else 0))
     rot = 0 if rope_tab is None else rope_tab.numel()
-    desc = capi.PrepDesc(n_heads, n_kv, hd, rot, pos, flags, cap, eps, 0)
+    return capi.PrepDesc(n_heads, n_kv, hd, rot, pos, flags, cap, eps, 0)
+
+
+def decode_layer(qg: torch.Tensor, k_raw: torch.Tensor, v_raw: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, *, pos: int, rope_tab: torch.Tensor | None,
+                 q_norm_w: torch.Tensor | None = None, k_norm_w: torch.Tensor | None = None,
+                 gated: bool = True, q_norm_add_one: bool = False, k_norm_add_one: bool = False,
+                 rope_interleaved: bool = False, eps: float = 1e-6, trunc_store: bool = False,
+                 scale: float = 0.0, n_splits: int = 0, out: torch.Tensor | None = None,
+                 kv_out: torch.Tensor | None = None, partial_ws: torch.Tensor | None = None):
+    """The attention of one decode token with its prep (nexus_hip_attn_decode_layer): the
+    arguments of decode_prep, plus the scale (0: 1/sqrt(hd)) and the split count (0: the
+    library's choice).  Row `pos` of the caches is written; rows [0, pos] are attended.
+    Returns (out [n_heads, hd] gated attention output, kv_out [2, n_kv, hd])."""
+    desc = _prep_desc(qg, k_raw, v_raw, k_cache, v_cache, pos=pos, rope_tab=rope_tab, q_norm_w=q_norm_w,
+                      k_norm_w=k_norm_w, gated=gated, q_norm_add_one=q_norm_add_one, k_norm_add_one=k_norm_add_one,
+                      rope_interleaved=rope_interleaved, eps=eps, trunc_store=trunc_store)
+    n_heads, n_kv, hd = desc.n_heads, desc.n_kv_heads, desc.head_dim
     dev = qg.device
-    q_out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev) if q_out is None else q_out
-    if gated and gate_out is None:
-        gate_out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev)
+    for name, t, shape in (("out", out, (n_heads, hd)), ("kv_out", kv_out, (2, n_kv, hd))):
+        if t is not None and (t.device != dev or t.dtype != torch.float32 or not t.is_contiguous()
+                              or tuple(t.shape) != shape):
+            raise ValueError(f"{name} must be a contiguous float32 {shape} tensor on {dev}")
+    out = torch.empty(n_heads, hd, dtype=torch.float32, device=dev) if out is None else out
     kv_out = torch.empty(2, n_kv, hd, dtype=torch.float32, device=dev) if kv_out is None else kv_out
+    splits = n_splits if n_splits > 0 else capi.decode_layer_default_splits(desc)
+    need = capi.decode_layer_ws_bytes(desc, splits)
+    if need == 0:
+        raise ValueError(capi.last_error() or "unsupported decode layer shape")
+    if partial_ws is None or partial_ws.numel() * partial_ws.element_size() < need:
+        partial_ws = torch.empty(need // 4, dtype=torch.float32, device=dev)
     ptr = lambda t: 0 if t is None else t.data_ptr()
-    capi.decode_prep_raw(desc, qg.data_ptr(), k_raw.data_ptr(), v_raw.data_ptr(), ptr(q_norm_w), ptr(k_norm_w),
-                         ptr(rope_tab), q_out.data_ptr(), ptr(gate_out if gated else None), k_cache.data_ptr(),
-                         v_cache.data_ptr(), kv_out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
-    return q_out, (gate_out if gated else None), kv_out
+    capi.decode_layer_raw(desc, scale, qg.data_ptr(), k_raw.data_ptr(), v_raw.data_ptr(), ptr(q_norm_w),
+                          ptr(k_norm_w), ptr(rope_tab), k_cache.data_ptr(), v_cache.data_ptr(), kv_out.data_ptr(),
+                          out.data_ptr(), partial_ws.data_ptr(), splits, torch.cuda.current_stream(dev).cuda_stream)
+    return out, kv_out
 
 
 # ------------------------------------------------------------------ KV session files

@@ -38,11 +38,13 @@ int shim_attention_flash_gpu(const float* q, float* out, int hq, int hkv, int hd
 
 // q35_attention with the host cache as one array [n_kv][host_cap][hd] (per-head pointers
 // built here) and device pointers for qg / k_raw / v_raw / out.
-int shim_q35_attention(const void* owner, int layer, int n_heads, int n_kv, int hd, int rot, int pos, float eps,
-                       float scale, int has_gate, int interleaved, const float* q_norm, const float* k_norm, int q_zc,
-                       int k_zc, const float* tab, const uint16_t* k_host, const uint16_t* v_host,
-                       long long host_cap, int host_tokens, int host_synced, const float* qg, const float* k_raw,
-                       const float* v_raw, float* out, float* kv_out, unsigned* mirror_valid, void* stream)
+// async_kv_slot >= 0: the chained form (kv_out unused; the K/V land in that chain slot).
+int shim_q35_attention_slot(const void* owner, int layer, int n_heads, int n_kv, int hd, int rot, int pos, float eps,
+                            float scale, int has_gate, int interleaved, const float* q_norm, const float* k_norm,
+                            int q_zc, int k_zc, const float* tab, const uint16_t* k_host, const uint16_t* v_host,
+                            long long host_cap, int host_tokens, int host_synced, const float* qg, const float* k_raw,
+                            const float* v_raw, float* out, float* kv_out, unsigned* mirror_valid, void* stream,
+                            int async_kv_slot)
 {
     if (n_kv <= 0 || n_kv > 64) return 0;
     const uint16_t* kp[64];
@@ -72,7 +74,32 @@ int shim_q35_attention(const void* owner, int layer, int n_heads, int n_kv, int 
     d.v_host = vp;
     d.host_tokens = (uint32_t)host_tokens;
     d.host_synced = (uint32_t)host_synced;
-    return backend().q35_attention(d, qg, k_raw, v_raw, out, kv_out, mirror_valid, (nexus_stream_t)stream) ? 1 : 0;
+    return backend().q35_attention(d, qg, k_raw, v_raw, out, kv_out, mirror_valid, (nexus_stream_t)stream,
+                                   async_kv_slot)
+               ? 1
+               : 0;
+}
+
+int shim_q35_attention(const void* owner, int layer, int n_heads, int n_kv, int hd, int rot, int pos, float eps,
+                       float scale, int has_gate, int interleaved, const float* q_norm, const float* k_norm, int q_zc,
+                       int k_zc, const float* tab, const uint16_t* k_host, const uint16_t* v_host,
+                       long long host_cap, int host_tokens, int host_synced, const float* qg, const float* k_raw,
+                       const float* v_raw, float* out, float* kv_out, unsigned* mirror_valid, void* stream)
+{
+    return shim_q35_attention_slot(owner, layer, n_heads, n_kv, hd, rot, pos, eps, scale, has_gate, interleaved,
+                                   q_norm, k_norm, q_zc, k_zc, tab, k_host, v_host, host_cap, host_tokens, host_synced,
+                                   qg, k_raw, v_raw, out, kv_out, mirror_valid, stream, -1);
+}
+
+int shim_chain_end(void) { return backend().chain_end() ? 1 : 0; }
+int shim_chain_is_open(void) { return backend().chain_is_open() ? 1 : 0; }
+// copies n floats of chain slot `slot` into dst; 0 when the slot has no memory
+int shim_chain_kv(int slot, float* dst, int n)
+{
+    const float* p = backend().chain_kv_ptr(slot);
+    if (!p) return 0;
+    for (int i = 0; i < n; ++i) dst[i] = p[i];
+    return 1;
 }
 
 void shim_q35_kv_drop(const void* owner, int layer) { backend().q35_kv_drop(owner, layer); }

@@ -35,6 +35,14 @@ def shim():
                                            _u16p, _u16p, ctypes.c_longlong, _i, _i, _vp, _vp, _vp, _vp, _f32p,
                                            ctypes.POINTER(ctypes.c_uint), _vp]
         lib.shim_q35_attention.restype = _i
+        slot_args = list(lib.shim_q35_attention.argtypes)
+        slot_args[25] = _vp                             # kv_out: unused (null) in the chained form
+        lib.shim_q35_attention_slot.argtypes = slot_args + [_i]
+        lib.shim_q35_attention_slot.restype = _i
+        lib.shim_chain_end.restype = _i
+        lib.shim_chain_is_open.restype = _i
+        lib.shim_chain_kv.argtypes = [_i, _f32p, _i]
+        lib.shim_chain_kv.restype = _i
         lib.shim_q35_kv_drop.argtypes = [_vp, _i]
         lib.shim_set_gpu_kv_mb.argtypes = [_i]
         lib.shim_kv_mirror_used.restype = ctypes.c_size_t
@@ -309,3 +317,65 @@ def test_mirror_rne_store(hip):
     finally:
         lib.shim_set_mirror_store_rne(0)
         lib.shim_q35_kv_drop(owner, -1)
+
+
+@pytest.mark.gpu
+def test_chained_layers_join_like_q35_chain_flush(hip):
+    """Layers chained without waiting (async_kv_slot = layer), as Transformer::forward runs
+    consecutive GPU layers, then one join that stores every slot's K/V into its host cache
+    (q35_chain_flush, transformer.h:10083-10100).  Every output and slot matches the CPU path;
+    the next token, synchronous, sees the rows the chained calls stored in the mirrors."""
+    import torch
+
+    rng = np.random.default_rng(55)
+    lib = shim()
+    lib.shim_set_gpu_kv_mb(-1)
+    owner = 0x7001
+    layers = [Layer(rng, host_cap=2048) for _ in range(4)]
+    for L in layers:
+        fill_prompt(L, rng, 900)
+    for pos in (900, 901):                              # two tokens of four chained layers each
+        pending = []
+        for li, L in enumerate(layers):
+            hq, nkv, hd = L.n_heads, L.n_kv, L.hd
+            qg = (rng.standard_normal((hq, 2 * hd)) * 2).astype(np.float32)
+            kraw = (rng.standard_normal((nkv, hd)) * 2).astype(np.float32)
+            vraw = rng.standard_normal((nkv, hd)).astype(np.float32)
+            tab = L.table(pos)
+            t = lambda x: torch.from_numpy(x).cuda()
+            qg_d, k_d, v_d = t(qg), t(kraw), t(vraw)
+            out_d = torch.full((hq, hd), 7.0, dtype=torch.float32, device="cuda")
+            mv = ctypes.c_uint(0)
+            h = L.host
+            ok = lib.shim_q35_attention_slot(owner, li, hq, nkv, hd, L.rot, pos, 1e-6, 0.0, 1, 0, L.qnw.ctypes.data,
+                                             L.knw.ctypes.data, 1, 1, tab.ctypes.data, h.k.reshape(-1),
+                                             h.v.reshape(-1), h.k.shape[1], h.n_tokens, min(h.mirror_valid, pos),
+                                             qg_d.data_ptr(), k_d.data_ptr(), v_d.data_ptr(), out_d.data_ptr(), None,
+                                             ctypes.byref(mv), torch.cuda.current_stream().cuda_stream, li)
+            assert ok == 1, lib.shim_last_decline()
+            assert mv.value == pos + 1
+            pending.append((L, li, qg, kraw, vraw, tab, out_d, (qg_d, k_d, v_d), mv.value))
+        assert lib.shim_chain_is_open() == 1
+        assert lib.shim_chain_end() == 1                # the join
+        assert lib.shim_chain_is_open() == 0
+        for L, li, qg, kraw, vraw, tab, out_d, _, mvv in pending:
+            hq, nkv, hd = L.n_heads, L.n_kv, L.hd
+            kv = np.zeros((2, nkv, hd), np.float32)
+            assert lib.shim_chain_kv(li, kv.reshape(-1), kv.size) == 1
+            r_q, r_gate, _, _, r_kv = O.decode_prep(qg, kraw, vraw, L.qnw, L.knw, tab, n_heads=hq, n_kv=nkv, hd=hd,
+                                                    rot=L.rot, flags=L.flags(), eps=1e-6, pos=0, cap=1)
+            np.testing.assert_allclose(kv, r_kv, rtol=1e-5, atol=2e-5)
+            L.host.store(pos, kv)                       # kvcache_.store + set_mirror_valid at the flush
+            L.host.mirror_valid = mvv
+            ref = O.attn_batch(r_q[None], np.ascontiguousarray(L.host.k[:, :pos + 1]),
+                               np.ascontiguousarray(L.host.v[:, :pos + 1]), n_kv_heads=nkv, n_ctx=pos + 1,
+                               q_base_pos=pos, n_threads=8)[0]
+            ref = O.gate_mul(ref, r_gate)
+            got = out_d.cpu().numpy()
+            ma, rl = O.max_abs(got, ref), O.rel_l2(got, ref)
+            print(f"[chain] pos={pos} layer={li} max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+            assert ma < 2e-3 and rl < 1e-3
+    for li, L in enumerate(layers):
+        step(L, rng, 902, owner, layer_id=li)           # synchronous, over the rows the chain stored
+        assert_mirror_equals_host(L, owner, 903, layer_id=li)
+    lib.shim_q35_kv_drop(owner, -1)
