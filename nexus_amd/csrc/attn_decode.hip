@@ -326,21 +326,14 @@ decode_ring_kernel(DecodeArgs a)
             for (int j = 0; j < PER; ++j) lds_st32(qaddr(r, lane + 64 * j), xq[i][j]);
         }
         if (pos_wg && wave < 2) {
-            // the new row: K normed and rotated, V as given; stored as the cache stores it
+            // the new row: K normed and rotated, V as given, in the cache's f16 conversion (its
+            // global stores wait for the end of the kernel: issued here, they would hold up this
+            // workgroup's first wait on its ring loads)
             if (wave == 0) prep_head(xn, (a.prep_flags & kPrepNoKNorm) == 0, (a.prep_flags & kPrepKZeroCentred) != 0, wk);
             const bool trunc = (a.prep_flags & kPrepTruncStore) != 0;
-            uint16_t* dst = (wave == 0 ? a.kc : a.vc) + ((size_t)kvh * a.kv_stride + a.q_base) * HD;
-            float* echo = a.kv_out + ((size_t)wave * a.n_kv_heads + kvh) * HD;
 #pragma unroll
-            for (int j = 0; j < PER; ++j) {
-                const int d = lane + 64 * j;
-                const uint16_t bits = trunc ? f16_trunc_bits(xn[j]) : f16_rne_bits(xn[j]);
-                if (rg == 0) {                                  // one row group stores it
-                    dst[d] = bits;
-                    echo[d] = xn[j];
-                }
-                lds_st16(newrow + 2 * (wave * HD + d), bits);
-            }
+            for (int j = 0; j < PER; ++j)
+                lds_st16(newrow + 2 * (wave * HD + lane + 64 * j), trunc ? f16_trunc_bits(xn[j]) : f16_rne_bits(xn[j]));
         }
         lgkm_wait_all();
         __builtin_amdgcn_s_barrier();
@@ -548,6 +541,17 @@ decode_ring_kernel(DecodeArgs a)
     // stages issued past the split are still landing in LDS: drain them before the
     // workgroup's LDS can be handed to another workgroup
     vm_wait<0>();
+    if (PREP && pos_wg && wave < 2 && rg == 0) {       // one row group stores the new row
+        const bool trunc = (a.prep_flags & kPrepTruncStore) != 0;
+        uint16_t* dst = (wave == 0 ? a.kc : a.vc) + ((size_t)kvh * a.kv_stride + a.q_base) * HD;
+        float* echo = a.kv_out + ((size_t)wave * a.n_kv_heads + kvh) * HD;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int d = lane + 64 * j;
+            dst[d] = trunc ? f16_trunc_bits(xn[j]) : f16_rne_bits(xn[j]);
+            echo[d] = xn[j];
+        }
+    }
 
     // ---- row sums across the four lanes of a row; lane (row n, group g) holds dims
     // 16 dt + 4 g + (0..3) of row n
