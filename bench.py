@@ -283,6 +283,36 @@ def copy_calibration(steps: int, warmup: int, nbytes: int = 256 << 20) -> None:
         f"(read+write), {nbytes / 1024:.0f} KiB read and written per launch")
 
 
+def gemm_ceiling(steps: int, warmup: int, n: int = 8192) -> dict:
+    """A plain library f16 GEMM (torch.matmul, n x n x n, f32 accumulate) on N(0,1) operands and
+    on all-zero operands: the matrix-core rate this GPU sustains under full load for data like the
+    attention inputs, beside the published dense peak.  The clock follows the power limit and the
+    matrix cores' power follows their operand data, so the two rates differ."""
+    import torch
+
+    res = {"shape": [n, n, n], "dtype": "f16"}
+    for tag, fill in (("normal", lambda t: t.normal_()), ("zeros", lambda t: t.zero_())):
+        a = fill(torch.empty(n, n, dtype=torch.float16, device="cuda"))
+        b = fill(torch.empty(n, n, dtype=torch.float16, device="cuda"))
+        c = torch.empty(n, n, dtype=torch.float16, device="cuda")
+        warm_up(lambda i: torch.matmul(a, b, out=c), warmup)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(steps):
+            torch.matmul(a, b, out=c)
+        s1.record()
+        s1.synchronize()
+        ms = s0.elapsed_time(s1) / steps
+        res[f"{tag}_tflops"] = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        res[f"{tag}_ms"] = ms
+        del a, b, c
+    res["normal_frac_of_peak"] = res["normal_tflops"] / MFMA_F16_PEAK_TFLOPS
+    log(f"[bench] f16 GEMM {n}^3: N(0,1) operands {res['normal_tflops']:.0f} TFLOP/s, zeros "
+        f"{res['zeros_tflops']:.0f} TFLOP/s ({100 * res['normal_frac_of_peak']:.1f}% / "
+        f"{100 * res['zeros_tflops'] / MFMA_F16_PEAK_TFLOPS:.1f}% of the dense peak)")
+    return res
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
@@ -483,9 +513,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy", "decode_layer"], default=None,
+    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy", "decode_layer", "gemm"], default=None,
                     help="measure one config only (for profiling runs); 'copy' runs a plain "
-                         "device copy of 256 MiB that calibrates the FETCH_SIZE/WRITE_SIZE counters")
+                         "device copy of 256 MiB that calibrates the FETCH_SIZE/WRITE_SIZE counters; "
+                         "'gemm' a library f16 GEMM on N(0,1) and on zero operands (the attainable "
+                         "matrix-core rate)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -508,6 +540,9 @@ def main() -> int:
     if args.only == "decode_layer":
         measure_decode_layer(args.steps, args.warmup)
         return 0
+    if args.only == "gemm":
+        gemm_ceiling(args.steps, args.warmup)
+        return 0
     if args.only:
         measure(args.only, args.steps, args.warmup)
         return 0
@@ -525,6 +560,7 @@ def main() -> int:
     extra["cap2"] = measure("cap2", args.steps, args.warmup, check=True)
     extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup, check=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
+    extra["gemm_ceiling"] = gemm_ceiling(max(5, args.steps // 5), args.warmup)
 
     cpu = None
     if not args.no_cpu_baseline:
