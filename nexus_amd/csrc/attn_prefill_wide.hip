@@ -230,8 +230,8 @@ prefill_wide_kernel(PrefillArgs a)
     const int rw = wave % L::RWAVES, kg = wave / L::RWAVES;
 
     // ---- work item: (kv head, query block [heaviest first], q head in group, key split)
-    const int item = xcd_remap(blockIdx.x, a.n_items);
     const int per_kv = a.group * a.n_qblocks * a.n_splits;
+    const int item = xcd_remap_kv(blockIdx.x, a.n_items, a.n_kv_heads, per_kv, a.n_splits);
     const int kvh = item / per_kv;
     int r = item - kvh * per_kv;
     const int qb = a.n_qblocks - 1 - r / (a.group * a.n_splits);
