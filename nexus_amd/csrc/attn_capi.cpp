@@ -584,7 +584,9 @@ int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, con
     if (items > INT_MAX) return capi_fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
     const bool q32 = desc->q_dtype == NEXUS_DT_F32, o32 = desc->o_dtype == NEXUS_DT_F32;
-    const hipError_t e = nxa::launch_prefill_wide(a, desc->head_dim, plan.ks, q32, o32, is_ext(desc), s);
+    // the softcap form (EXT) only when there is a softcap: a sliding window is masking, which the
+    // plain form does too
+    const hipError_t e = nxa::launch_prefill_wide(a, desc->head_dim, plan.ks, q32, o32, desc->softcap > 0.f, s);
     if (e != hipSuccess) return capi_fail(NEXUS_E_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
     if (splits > 1) {
         const int rc2 = launch_combine_for(desc, (float*)workspace, out, gate, splits, s);

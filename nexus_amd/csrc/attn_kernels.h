@@ -136,7 +136,8 @@ __host__ __device__ inline size_t part_ml(int split, long long row, long long n_
 
 // Each launcher returns hipSuccess or the launch error; shapes are validated by the caller.
 // Pipelined prefill: causal shapes at head dims 64, 128, 192, 256 (KS = 2 at 64 and 128 only),
-// with softcap and sliding window when `ext`; n_qblocks counts prefill_wide_rows(ks)-row blocks.
+// sliding window in either form, softcap when `ext`; n_qblocks counts prefill_wide_rows(ks)-row
+// blocks.
 int prefill_wide_rows(int ks);
 hipError_t launch_prefill_wide(const PrefillArgs& a, int head_dim, int ks, bool q_f32, bool o_f32, bool ext,
                                hipStream_t stream);

@@ -32,8 +32,9 @@
 //    -m (raw units), so a probability is exp2(scale * log2(e) * S): the scale is applied in
 //    f32, never folded into an f16 operand.  The running max moves lazily (only past a 2^8
 //    margin), the row max is v_max3 + v_permlane32_swap, row sums are fp32 adds of the
-//    probabilities.  EXT: accumulators seeded with 0, and the VALU turns each raw score into
-//    softcap * tanh(x scale / softcap) * log2(e) - m (or x scale log2(e) - m) before the row max.
+//    probabilities.  EXT (softcap): accumulators seeded with 0, and the VALU turns each raw
+//    score into softcap * tanh(x scale / softcap) * log2(e) - m before the row max.  A sliding
+//    window is masking only, in both forms.
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -247,7 +248,7 @@ prefill_wide_kernel(PrefillArgs a)
     const int q0 = qb * BM;
     const int k_hi = min(a.q_base + min(q0 + BM, a.n_query) - 1, a.n_ctx - 1);
     const int n_tiles = k_hi / BN + 1;
-    const bool swa = EXT && a.sliding_window > 0;
+    const bool swa = a.sliding_window > 0;
     const int t_lo = swa ? min(max(0, a.q_base + q0 + 1 - a.sliding_window) / BN, n_tiles) : 0;
     const int tps = (n_tiles - t_lo + a.n_splits - 1) / a.n_splits;
     const int t0 = min(t_lo + split * tps, n_tiles), t1 = min(t0 + tps, n_tiles);

@@ -98,6 +98,10 @@ PREFILL_CASES = [
     (16, 2, 256, 300, 1000, 0, True, True, 0, 50.0),     # hd 256 softcap in key splits
     (8, 2, 64, 200, 5000, 0, True, False, 1000, 0.0),    # hd 64 window in key splits
     (8, 2, 256, 256, 0, 0, False, True, 100, 30.0),      # hd 256 window + softcap, cold
+    # a window without softcap takes the plain form (accumulators seeded with -m, masking only)
+    (16, 2, 256, 300, 40, 0, True, True, 150, 0.0),      # hd 256 window, AGPR form
+    (12, 4, 192, 200, 100, 0, False, False, 90, 0.0),    # hd 192 window, f32 q/o
+    (64, 8, 128, 512, 300, 0, False, True, 256, 0.0),    # window, 128-row blocks, f32 q (residual MFMA)
     # 64-row blocks at one to one and a half per CU (cfg2's regime)
     (32, 8, 128, 512, 100, 0, True, True, 0, 0.0),       # exactly one block per CU
     (40, 8, 128, 520, 300, 0, False, False, 0, 0.0),     # 360 blocks, ragged last block
@@ -178,6 +182,7 @@ GATED_PREFILL_CASES = [
     (6, 2, 192, 70, 10, True, True, 0, 0.0, True),         # pipelined kernel, hd 192 (AGPR form)
     (8, 1, 256, 64, 4000, True, False, 0, 0.0, True),      # hd 256 in 16 key splits: gate in the row combine
     (6, 2, 192, 70, 2000, False, True, 300, 20.0, True),   # hd 192 key splits, window + softcap
+    (8, 2, 128, 80, 0, True, True, 40, 0.0, True),         # window without softcap, 64-row blocks
     (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # pipelined kernel, softcap
     (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # softcapped key split + combine
     (40, 8, 128, 520, 300, True, True, 0, 0.0, True),      # pipelined kernel, 360 64-row blocks
