@@ -152,11 +152,42 @@ __device__ __forceinline__ f32x2 gate2(const float* gate, size_t off)
 // x * inv * (1 + w), inv = 1 / sqrt(mean(x^2) + eps).  RoPE pairs are (i, i + rot/2)
 // (rotate_half) or (2i, 2i + 1) (interleaved), the two layouts of rope_apply
 // (src/model/attention.h:593-608), cos at tab[i] and sin at tab[rot/2 + i].
+// x of the lane a DPP control selects (gfx9 controls; every lane is a valid source)
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1, 0, 3, 2]: lane l ^ 1
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2, 3, 0, 1]: lane l ^ 2
+constexpr int kDppHalfMirror = 0x141;   // row_half_mirror: lane 7 - i within 8 lanes
+constexpr int kDppMirror = 0x140;       // row_mirror: lane 15 - i within 16 lanes
+// x of lane l ^ 32 (v_permlane32_swap leaves x[l ^ 32] in the second register of lanes 0-31
+// and in the first of lanes 32-63)
+__device__ __forceinline__ float lane_xor32(float x, int lane)
+{
+    float a = x, b = x;
+    swap_halves32(a, b);
+    return lane < 32 ? b : a;
+}
+__device__ __forceinline__ float lane_xor16(float x, int lane)
+{
+    float a = x, b = x;
+    swap_rows16(a, b);
+    return (lane & 16) == 0 ? b : a;
+}
+// Sum over the 64 lanes, the same value in every lane, on the VALU: lanes l ^ 1 and l ^ 2 (quad
+// permutes), then the mirrors within 8- and 16-lane rows (each quad, then each half row, holds
+// one value by then, so a mirror adds the neighbouring one), then the other 16-lane row and the
+// other half of the wave (permlane swaps).  Both lanes of every pair add the same two operands.
 __device__ __forceinline__ float prep_wave_sum(float x)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-    return x;
+    x += dpp_mov<kDppXor1>(x);
+    x += dpp_mov<kDppXor2>(x);
+    x += dpp_mov<kDppHalfMirror>(x);
+    x += dpp_mov<kDppMirror>(x);
+    x = sum_xor16(x);
+    return sum_xor32(x);
 }
 __device__ __forceinline__ float prep_norm_inv(float sum_sq, int hd, float eps)
 {
@@ -181,6 +212,44 @@ __device__ __forceinline__ float prep_rope(int d, float x, float p, float c, flo
 {
     if (interleaved) return (d & 1) == 0 ? x * c - p * s : p * s + x * c;
     return d < (rot >> 1) ? x * c - p * s : x * c + p * s;
+}
+// RoPE partners p[j] of the elements x[j] = element lane + 64 j below rot, taken from registers
+// where the pairing allows it: interleaved pairs are lanes l, l ^ 1; rotate_half pairs d, d + rot/2
+// are lanes l, l ^ 16 (rot 32) or l ^ 32 (rot 64), or elements j, j ^ 1 (rot 128) or j ^ 2 (rot 256)
+// of one lane.  False for other rotations (the caller exchanges through LDS).  Wave-uniform.
+template <int PER>
+__device__ __forceinline__ bool prep_rope_partners(const float (&x)[PER], float (&p)[PER], int lane, int rot,
+                                                   bool interleaved)
+{
+    if (interleaved) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) p[j] = dpp_mov<kDppXor1>(x[j]);
+        return true;
+    }
+    switch (rot) {
+    case 32:
+        p[0] = lane_xor16(x[0], lane);
+        return true;
+    case 64:
+        p[0] = lane_xor32(x[0], lane);
+        return true;
+    case 128:
+        if constexpr (PER >= 2) {
+            p[0] = x[1];
+            p[1] = x[0];
+            return true;
+        }
+        return false;
+    case 256:
+        if constexpr (PER >= 4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = x[j ^ 2];
+            return true;
+        }
+        return false;
+    default:
+        return false;
+    }
 }
 
 // f32 -> f16 bits, round to nearest even: the hardware conversion, which matches

@@ -297,20 +297,23 @@ decode_ring_kernel(DecodeArgs a)
                 for (int j = 0; j < PER; ++j) x[j] = prep_norm_apply(x[j], inv, w[j], add_one);
             }
             if (a.rot > 0) {
-#pragma unroll
-                for (int j = 0; j < PER; ++j)
-                    if (lane + 64 * j < a.rot) lds_st32(scratch + 4 * (lane + 64 * j), x[j]);
-                lgkm_wait_all();
                 float pr[PER];
+                if (!prep_rope_partners(x, pr, lane, a.rot, inter)) {      // other rotations: via LDS
 #pragma unroll
-                for (int j = 0; j < PER; ++j) {
-                    const int d = lane + 64 * j;
-                    pr[j] = lds_ld32(scratch + 4 * (d < a.rot ? prep_rope_partner(d, a.rot, inter) : 0));
+                    for (int j = 0; j < PER; ++j)
+                        if (lane + 64 * j < a.rot) lds_st32(scratch + 4 * (lane + 64 * j), x[j]);
+                    lgkm_wait_all();
+#pragma unroll
+                    for (int j = 0; j < PER; ++j) {
+                        const int d = lane + 64 * j;
+                        pr[j] = lds_ld32(scratch + 4 * (d < a.rot ? prep_rope_partner(d, a.rot, inter) : 0));
+                    }
+                    lgkm_wait_all();
+#pragma unroll
+                    for (int j = 0; j < PER; ++j) after_wait(pr[j]);
                 }
-                lgkm_wait_all();
 #pragma unroll
                 for (int j = 0; j < PER; ++j) {
-                    after_wait(pr[j]);
                     const int d = lane + 64 * j;
                     if (d < a.rot) x[j] = prep_rope(d, x[j], pr[j], rc[j], rs[j], a.rot, inter);
                 }

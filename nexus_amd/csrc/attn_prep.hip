@@ -8,9 +8,10 @@
 // the f32 results agree with the CPU path to rounding.
 //
 // MI355X shape: the whole op moves a few hundred KB, so it is launch-latency bound; one
-// 64-lane wave per head keeps every reduction inside the wave (no LDS tree, no barriers
-// beyond the one before the RoPE partner reads) and lets all heads run at once on
-// separate CUs.  Lane l owns elements l, l + 64, ... (coalesced 256-byte rows).
+// 64-lane wave per head keeps every reduction inside the wave (DPP and permlane steps on the
+// VALU, no LDS) and lets all heads run at once on separate CUs; RoPE partners come from
+// registers for the usual rotations and through LDS (one barrier) for the others.  Lane l owns
+// elements l, l + 64, ... (coalesced 256-byte rows).
 #include "attn_common.h"
 #include "attn_kernels.h"
 
@@ -62,20 +63,27 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(PrepArgs a)
         }
         const int rot = a.rot;
         if (rot > 0) {
-#pragma unroll
-            for (int j = 0; j < kPrepPer; ++j) {
-                const int d = lane + 64 * j;
-                if (d < rot) row[d] = x[j];
-            }
-            __syncthreads();
             const bool inter = (a.flags & kPrepInterleaved) != 0;
+            float pr[kPrepPer];
+            if (!prep_rope_partners(x, pr, lane, rot, inter)) {   // other rotations: via LDS
+#pragma unroll
+                for (int j = 0; j < kPrepPer; ++j) {
+                    const int d = lane + 64 * j;
+                    if (d < rot) row[d] = x[j];
+                }
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < kPrepPer; ++j) {
+                    const int d = lane + 64 * j;
+                    pr[j] = d < rot ? row[prep_rope_partner(d, rot, inter)] : 0.f;
+                }
+            }
 #pragma unroll
             for (int j = 0; j < kPrepPer; ++j) {
                 const int d = lane + 64 * j;
                 if (d >= rot) continue;
                 const int ci = prep_rope_cos_index(d, rot, inter);
-                x[j] = prep_rope(d, x[j], row[prep_rope_partner(d, rot, inter)], a.tab[ci], a.tab[(rot >> 1) + ci], rot,
-                                 inter);
+                x[j] = prep_rope(d, x[j], pr[j], a.tab[ci], a.tab[(rot >> 1) + ci], rot, inter);
             }
         }
     }

@@ -50,6 +50,10 @@ PREP_CASES = [
     (6, 3, 80, 32, capi.PREP_NO_GATE, 1, 2),                                             # ragged head (80 dims)
     (16, 2, 256, 64, capi.PREP_Q_NORM_ADD_ONE | capi.PREP_K_NORM_ADD_ONE | capi.PREP_TRUNC_STORE, 100, 128),
     (12, 4, 192, 96, capi.PREP_ROPE_INTERLEAVED | capi.PREP_K_NORM_ADD_ONE, 5, 6),       # gated, interleaved
+    # rotations whose partners are exchanged through LDS (the others come from registers)
+    (12, 4, 192, 96, capi.PREP_K_NORM_ADD_ONE, 5, 6),                                    # rotate_half, rot 96
+    (8, 2, 256, 192, capi.PREP_Q_NORM_ADD_ONE | capi.PREP_NO_GATE, 40, 64),              # rot 192
+    (4, 2, 64, 48, capi.PREP_NO_GATE, 2, 8),                                              # rot 48, hd 64
 ]
 
 
@@ -134,6 +138,9 @@ LAYER_CASES = [
     (12, 4, 192, 96, capi.PREP_ROPE_INTERLEAVED | capi.PREP_K_NORM_ADD_ONE, 300, 320, 3),
     (64, 2, 128, 64, capi.PREP_Q_NORM_ADD_ONE | capi.PREP_K_NORM_ADD_ONE, 1000, 1024, 0),   # G = 32: two row tiles
     (64, 1, 64, 0, capi.PREP_TRUNC_STORE, 2500, 2560, 0),                  # G = 64: two row groups, no RoPE
+    (12, 4, 192, 96, capi.PREP_K_NORM_ADD_ONE, 300, 320, 3),              # rotate_half rot 96: partners via LDS
+    (16, 2, 256, 192, capi.PREP_Q_NORM_ADD_ONE | capi.PREP_K_NORM_ADD_ONE, 700, 768, 0),   # rot 192 via LDS
+    (16, 4, 128, 32, capi.PREP_NO_GATE, 50, 64, 2),                       # rot 32: partners lane ^ 16
 ]
 
 
