@@ -42,6 +42,9 @@ CONFIGS = {
                  desc="decode 1 token, 40q/8kv, hd128, 61440 keys, 64 splits, f32 LSE combine"),
     "q35p": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=8192, base=0, n_ctx=8192, q="f16", o="f16",
                  desc="cold prefill 8192 tokens, 16q/2kv, hd256 (the Qwen3.5 full-attention layer's shape)"),
+    "cfg2q32": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=512, base=4096, n_ctx=4608, q="f32", o="f32",
+                    desc="cfg2's shape with f32 Q and f32 out (the engine's attention_flash_gpu form: Q as an f16 high "
+                         "part plus its f16 residual)"),
     "cap2": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=512, base=4096, n_ctx=4608, q="f16", o="f16", cap=30.0,
                  desc="cfg2's shape with logit softcap 30 (Gemma-style), f16 Q/K/V/O"),
     "swa3": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=8192, base=0, n_ctx=8192, q="f16", o="f16", sw=4096,
@@ -557,6 +560,7 @@ def main() -> int:
     extra["cfg5_warm"] = measure("cfg5", args.steps, args.warmup, rotate=False)
     extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup, check=True)
     extra["q35c"] = measure("q35c", args.steps, args.warmup, check=True)
+    extra["cfg2q32"] = measure("cfg2q32", args.steps, args.warmup, check=True)
     extra["cap2"] = measure("cap2", args.steps, args.warmup, check=True)
     extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup, check=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
