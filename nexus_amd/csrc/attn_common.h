@@ -294,20 +294,23 @@ __device__ __forceinline__ int xcd_remap(int b, int n_items)
 }
 
 // The same for causal query blocks ordered (kv head, heaviest first) in runs of per_kv per kv
-// head, one work item per block (no key splits).  With fewer than 8 kv heads, a contiguous
-// range per XCD would hand one XCD a kv head's heaviest blocks and another its lightest (they
-// differ in length up to n_qblocks-fold): when n_kv divides 8, each kv head gets its own 8 / n_kv
-// XCDs instead and deals its blocks over them round robin, so every XCD receives the same mix of
-// heavy and light blocks, heaviest first, and still reads only one kv head's K/V (measured on
-// MI355X, 16q/2kv hd 256, 8192 tokens cold: 970 -> 612 us).  Key-split items are near equal in
-// length and keep the contiguous ranges (512 queries over 32k keys in 4 splits: 305 vs 309 us).
+// head, one work item per block (no key splits).  Contiguous ranges would hand one XCD a kv
+// head's heaviest blocks and another its lightest whenever a kv head spans several XCDs or an
+// XCD boundary cuts through one (blocks differ in length up to n_qblocks-fold).  Instead the 8
+// XCDs form g = gcd(n_kv, 8) groups of 8 / g, each serving n_kv / g kv heads whose blocks it
+// deals round robin over its XCDs: every XCD gets the same mix of heavy and light blocks,
+// heaviest first within each kv head, and reads only its group's K/V.  With n_kv a multiple of
+// 8 this is the contiguous mapping (whole kv heads per XCD).  Measured on MI355X, 16q/2kv hd
+// 256, 8192 tokens cold: 970 -> 612 us.  Key-split items are near equal in length and keep the
+// contiguous ranges (512 queries over 32k keys in 4 splits: 305 vs 309 us).
 __device__ __forceinline__ int xcd_remap_kv(int b, int n_items, int n_kv, int per_kv, int n_splits)
 {
-    if (n_splits == 1 && n_kv < 8 && 8 % n_kv == 0) {
-        const int c = 8 / n_kv;                               // XCDs per kv head
-        if (per_kv % c == 0) {                                // n_items = 8 * (per_kv / c)
+    if (n_splits == 1) {
+        const int g = min(n_kv & -n_kv, 8);                   // gcd(n_kv, 8)
+        const int c = 8 / g;                                  // XCDs per group
+        if (per_kv % c == 0) {                                // n_items = 8 * (n_kv / g) * per_kv / c
             const int x = b & 7, t = b >> 3;
-            return (x / c) * per_kv + t * c + x % c;
+            return (x / c) * (n_kv / g) * per_kv + t * c + x % c;
         }
     }
     return xcd_remap(b, n_items);

@@ -106,6 +106,10 @@ PREFILL_CASES = [
     (32, 8, 128, 512, 100, 0, True, True, 0, 0.0),       # exactly one block per CU
     (40, 8, 128, 520, 300, 0, False, False, 0, 0.0),     # 360 blocks, ragged last block
     (36, 4, 64, 512, 700, 0, True, False, 200, 10.0),    # hd 64, window + softcap
+    # kv head counts that do not divide 8: XCD groups of several kv heads (work order only)
+    (24, 12, 128, 700, 0, 0, True, True, 0, 0.0),        # 12 kv heads: 4 groups of 3 on 2 XCDs each
+    (18, 6, 64, 1000, 50, 0, True, True, 0, 0.0),        # 6 kv heads: 2 groups of 3 on 4 XCDs each
+    (15, 3, 256, 600, 0, 0, True, False, 0, 0.0),        # 3 kv heads, hd 256: one group on 8 XCDs
 ]
 
 
