@@ -536,13 +536,16 @@ prefill_wide_kernel(PrefillArgs a)
             }
         }
     };
-    // EXT: the MFMAs leave raw scores q.k (accumulators seeded with 0); the VALU scales and
-    // softcaps them, converts to log2 units and subtracts the running max
-    const float cap_c1 = EXT && a.softcap > 0.f ? 2.f * kLog2e / a.softcap : 0.f;
+    // EXT: the MFMAs leave raw scores x = q.k (accumulators seeded with 0); the VALU turns each
+    // into softcap * tanh(x scale / softcap) * log2(e) - m = (c2 - m) - 2 c2 / (2^(x c1) + 1)
+    // with c1 = 2 log2(e) scale / softcap and c2 = softcap log2(e) (tanh(y) = 1 - 2 / (e^(2y) + 1),
+    // as softcap_log2): a multiply, v_exp_f32, an add, v_rcp_f32 and one fma per score
+    const bool capped = EXT && a.softcap > 0.f;
+    const float cap_c1 = capped ? 2.f * kLog2e * a.scale / a.softcap : a.scale * kLog2e;
     const float cap_c2 = a.softcap * kLog2e;
     auto ext_score = [&](float x, int rb) {
-        x *= a.scale;
-        return (a.softcap > 0.f ? softcap_log2(x, cap_c1, cap_c2) : x * kLog2e) - m_used[rb];
+        if (!capped) return x * cap_c1 - m_used[rb];
+        return __builtin_fmaf(-2.f * cap_c2, __builtin_amdgcn_rcpf(fast_exp2(x * cap_c1) + 1.f), cap_c2 - m_used[rb]);
     };
     // finish tile t's scores: mask if needed, row max, rescale
     auto finish_scores = [&](STile& sv, int t, float (&mx)[NB]) {
