@@ -526,7 +526,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's attention path runs on a single MI355X "
-              "(multi-GPU sharding is design-only, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(sharding over several GPUs is not built in this tier); run with --gpus 1", file=sys.stderr)
         return 2
 
     import torch

@@ -141,7 +141,7 @@ def test_workspace_sizes():
 
 
 def test_algorithmic_work_formulas():
-    # cfg2 / cfg3 pair counts from the survey: 2,228,480 and 33,558,528 pairs per head
+    # cfg2 / cfg3 visible (query, key) pairs per head: 512 queries after 4096 keys, 8192 cold
     assert capi.prefill_flops(40, 128, 512, 4096, 4608) == 4 * 128 * 40 * 2_228_480
     assert capi.prefill_flops(40, 128, 8192, 0, 8192) == 4 * 128 * 40 * 33_558_528
     assert capi.decode_bytes(8, 128, 61440, 40, 1) == 2 * 8 * 61440 * 128 * 2 + 40 * 128 * 8
