@@ -316,6 +316,33 @@ def gemm_ceiling(steps: int, warmup: int, n: int = 8192) -> dict:
     return res
 
 
+def read_reference(steps: int, warmup: int) -> dict:
+    """A plain library read for the decode sizes: torch's int64 max over 64 MiB of f16 data (the
+    K/V of the hd-256 decode at 32k keys; eight distinct buffers rotated past the Infinity Cache)
+    and over 1 GiB, each timed with HIP events.  The rate a library reduction reaches at 64 MiB,
+    with its launch and ramp, against the split-KV decode that reads the same bytes and computes."""
+    import torch
+
+    res = {"op": "torch int64 max over f16 data (read only)"}
+    for tag, mib, n_sets in (("64MiB", 64, 8), ("1GiB", 1024, 1)):
+        n = mib << 20
+        sets = [torch.randn(n // 2, device="cuda").half().view(torch.int64) for _ in range(n_sets)]
+        warm_up(lambda i: sets[i % n_sets].max(), warmup)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for i in range(steps):
+            sets[i % n_sets].max()
+        s1.record()
+        s1.synchronize()
+        us = s0.elapsed_time(s1) / steps * 1e3
+        res[f"{tag}_us"] = us
+        res[f"{tag}_tbs"] = n / (us * 1e-6) / 1e12
+        del sets
+    log(f"[bench] library read (torch int64 max): 64 MiB {res['64MiB_us']:.1f} us = {res['64MiB_tbs']:.2f} TB/s, "
+        f"1 GiB {res['1GiB_tbs']:.2f} TB/s")
+    return res
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
@@ -516,11 +543,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy", "decode_layer", "gemm"], default=None,
+    ap.add_argument("--only", choices=sorted(CONFIGS) + ["copy", "decode_layer", "gemm", "read"], default=None,
                     help="measure one config only (for profiling runs); 'copy' runs a plain "
                          "device copy of 256 MiB that calibrates the FETCH_SIZE/WRITE_SIZE counters; "
                          "'gemm' a library f16 GEMM on N(0,1) and on zero operands (the attainable "
-                         "matrix-core rate)")
+                         "matrix-core rate); 'read' a library read of 64 MiB and 1 GiB")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -546,6 +573,9 @@ def main() -> int:
     if args.only == "gemm":
         gemm_ceiling(args.steps, args.warmup)
         return 0
+    if args.only == "read":
+        read_reference(args.steps, args.warmup)
+        return 0
     if args.only:
         measure(args.only, args.steps, args.warmup)
         return 0
@@ -565,6 +595,7 @@ def main() -> int:
     extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup, check=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
     extra["gemm_ceiling"] = gemm_ceiling(max(5, args.steps // 5), args.warmup)
+    extra["read_reference"] = read_reference(args.steps, args.warmup)
 
     cpu = None
     if not args.no_cpu_baseline:
