@@ -170,12 +170,14 @@ size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
 // write + read per row and split plus a combine launch, which only pays off when the unsplit
 // grid leaves most CUs idle (measured on MI355X: 160 workgroups of 512 queries x 40 heads run
 // faster unsplit than in 3 splits; 320 pipelined workgroups of 64 queries x 40 heads in 2
-// splits take 96 us against 62 unsplit).  Below half a workgroup per CU, split so the grid
-// reaches about one workgroup per CU, each split keeping >= 4 key tiles of 64.
+// splits take 96 us against 62 unsplit).  Below half a workgroup per CU (head dims <= 128, two
+// workgroups per CU), or below one workgroup per CU (head dims 192 and 256, one per CU: a
+// 1024-token prompt tile of 16 heads is 128 workgroups, which left half the CUs idle), split so
+// the grid reaches about one workgroup per CU, each split keeping >= 4 key tiles of 64.
 int prefill_splits(const nexus_attn_desc* d, long long base)
 {
     const long long cus = device_cus();
-    if (2 * base >= cus) return 1;
+    if ((nxa::decode_wg_per_cu(d->head_dim) == 2 ? 2 * base : base) >= cus) return 1;
     long long s = cus / base;
     int kb, ke;
     key_range(d, &kb, &ke);

@@ -110,6 +110,7 @@ PREFILL_CASES = [
     (24, 12, 128, 700, 0, 0, True, True, 0, 0.0),        # 12 kv heads: 4 groups of 3 on 2 XCDs each
     (18, 6, 64, 1000, 50, 0, True, True, 0, 0.0),        # 6 kv heads: 2 groups of 3 on 4 XCDs each
     (15, 3, 256, 600, 0, 0, True, False, 0, 0.0),        # 3 kv heads, hd 256: one group on 8 XCDs
+    (16, 2, 256, 1024, 1024, 0, True, True, 0, 0.0),     # the engine's 1024-token tile at hd 256: 128 blocks in 2 splits
 ]
 
 
