@@ -51,6 +51,11 @@ CONFIGS = {
                  desc="cfg3's shape with a 4096-token sliding window (work counted over visible pairs)"),
     "q35c": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=512, base=32768, n_ctx=33280, q="f16", o="f16",
                  desc="chunked prefill 512 queries after 32768 cached tokens, 16q/2kv, hd256 (key splits + combine)"),
+    "tile3": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=1024, base=3072, n_ctx=4096, q="f16", o="f16",
+                  desc="the engine's 1024-token prompt tile (transformer.h:8551-8560) after 3072 cached tokens, "
+                       "40q/8kv, hd128"),
+    "q35t3": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=1024, base=3072, n_ctx=4096, q="f16", o="f16",
+                  desc="the engine's 1024-token prompt tile after 3072 cached tokens, 16q/2kv, hd256 (key splits)"),
     "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
                  desc="MTP verify 4 drafts at 32768 cached tokens, 16q/2kv, hd256, causal among drafts"),
 }
@@ -591,6 +596,8 @@ def main() -> int:
     extra["q35p"] = measure("q35p", max(5, args.steps // 5), args.warmup, check=True)
     extra["q35c"] = measure("q35c", args.steps, args.warmup, check=True)
     extra["cfg2q32"] = measure("cfg2q32", args.steps, args.warmup, check=True)
+    extra["tile3"] = measure("tile3", args.steps, args.warmup, check=True)
+    extra["q35t3"] = measure("q35t3", args.steps, args.warmup, check=True)
     extra["cap2"] = measure("cap2", args.steps, args.warmup, check=True)
     extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup, check=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
