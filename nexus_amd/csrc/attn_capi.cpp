@@ -217,9 +217,21 @@ PrefillPlan prefill_plan(const nexus_attn_desc* d)
     return p;
 }
 
+// Chunks short enough for the split-KV decode kernel.  It streams a kv head's K/V once per group
+// of 32 (query, head-in-group) rows (R groups), where the prefill kernel reads it once per q head
+// (G times) into 128-query blocks such a chunk barely fills.  Measured on MI355X (8-64 queries):
+// the decode kernel wins for one group at any length, while 2R <= G behind >= 8k keys (16q/2kv hd
+// 256, 16 queries over 8k: 22.8 vs 27.7 us) and while R < G behind >= 16k (8 queries over 32k: 29.7
+// vs 77.0 us; 40q/8kv hd 128, 24 over 32k: 66 vs 92); otherwise the prefill kernel's lower fixed
+// costs win (40q/8kv hd 128, 12 queries over 4k: 14.6 vs 16.2 us).
 bool small_query_path(const nexus_attn_desc* d)
 {
-    return decode_rows(d) <= (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
+    const long long per = (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
+    const long long groups = (decode_rows(d) + per - 1) / per;
+    const long long g = d->n_q_heads / d->n_kv_heads;
+    if (groups <= 1) return true;
+    if (d->n_ctx >= 16384 && groups < g) return true;
+    return d->n_ctx >= 8192 && 2 * groups <= g;
 }
 
 int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, const float* gate, int n_splits,
