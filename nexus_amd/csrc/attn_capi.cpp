@@ -197,24 +197,50 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // us).  Head dims 192 and 256 have the 128-row form only: the two-key-group form does not fit
 // one wave per SIMD's registers.  Either grid splits the key range over workgroups by the rule
 // above.
+// Packed rows: a chunk of at most 128 queries with several q heads per kv head can have its
+// blocks over the (query, head-in-group) pairs of each kv head instead of one padded block per q
+// head, so the group's heads share every K/V tile (read once per block, not once per q head) and
+// only the last block of a kv head is partly filled.  It pays behind long caches, where the
+// unpacked grid's G-fold K/V reads dominate, and is taken there (>= 16k keys) when its grid is at
+// least as large as the unpacked one or fills every CU (fewer blocks, so a smaller grid).
+// Measured on MI355X: 40q/8kv hd 128, 32/48/96 queries over 32k keys 90/92/160 -> 63/76/128 us;
+// behind 4-8k keys within +-10% either way; 16q/2kv hd 256, 32 queries over 8k packed into 64
+// workgroups instead of 256: 14% slower.
 struct PrefillPlan {
     int ks;
     int splits;
+    bool pack;
 };
 
-long long query_blocks(const nexus_attn_desc* d, long long rows)
+// Blocks of `rows` rows of a prefill grid (per q head, or per kv head when packed).
+long long query_blocks(const nexus_attn_desc* d, long long rows, bool pack)
 {
-    return (long long)d->n_q_heads * ((d->n_query + rows - 1) / rows);
+    const long long units = pack ? d->n_kv_heads : d->n_q_heads;
+    const long long n = pack ? (long long)d->n_query * (d->n_q_heads / d->n_kv_heads) : d->n_query;
+    return units * ((n + rows - 1) / rows);
+}
+
+PrefillPlan prefill_plan_for(const nexus_attn_desc* d, bool pack)
+{
+    PrefillPlan p{1, 1, pack};
+    const long long b1 = query_blocks(d, nxa::prefill_wide_rows(1), pack), cus = device_cus();
+    const bool ks2 = b1 <= cus || (b1 < 2 * cus && d->q_base_pos < d->n_query);
+    p.ks = ks2 && d->head_dim <= 128 ? 2 : 1;
+    p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks), pack));
+    return p;
+}
+
+long long prefill_plan_wgs(const nexus_attn_desc* d, const PrefillPlan& p)
+{
+    return query_blocks(d, nxa::prefill_wide_rows(p.ks), p.pack) * p.splits;
 }
 
 PrefillPlan prefill_plan(const nexus_attn_desc* d)
 {
-    PrefillPlan p{1, 1};
-    const long long b1 = query_blocks(d, nxa::prefill_wide_rows(1)), cus = device_cus();
-    const bool ks2 = b1 <= cus || (b1 < 2 * cus && d->q_base_pos < d->n_query);
-    p.ks = ks2 && d->head_dim <= 128 ? 2 : 1;
-    p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks)));
-    return p;
+    const PrefillPlan plain = prefill_plan_for(d, false);
+    if (d->n_query > 128 || d->n_q_heads == d->n_kv_heads || d->n_ctx < 16384) return plain;
+    const PrefillPlan packed = prefill_plan_for(d, true);
+    return prefill_plan_wgs(d, packed) >= std::min<long long>(prefill_plan_wgs(d, plain), device_cus()) ? packed : plain;
 }
 
 // Chunks short enough for the split-KV decode kernel.  It streams a kv head's K/V once per group
@@ -598,9 +624,11 @@ int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, con
     a.scale_log2 = a.scale * 1.4426950408889634f;
     a.softcap = desc->softcap;
     const long long rows = nxa::prefill_wide_rows(plan.ks);
-    a.n_qblocks = (int)((desc->n_query + rows - 1) / rows);
+    const long long row_space = plan.pack ? (long long)desc->n_query * a.group : desc->n_query;
+    a.pack = plan.pack ? 1 : 0;
+    a.n_qblocks = (int)((row_space + rows - 1) / rows);
     a.n_splits = splits;
-    const long long items = (long long)desc->n_q_heads * a.n_qblocks * splits;
+    const long long items = (long long)(plan.pack ? desc->n_kv_heads : desc->n_q_heads) * a.n_qblocks * splits;
     if (items > INT_MAX) return capi_fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
     const bool q32 = desc->q_dtype == NEXUS_DT_F32, o32 = desc->o_dtype == NEXUS_DT_F32;

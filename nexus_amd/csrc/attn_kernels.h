@@ -39,6 +39,8 @@ struct PrefillArgs {
     float scale_log2;               // scale * log2(e)
     float softcap;
     int n_qblocks, n_splits, n_items;
+    int pack;                       // non-zero: a block's rows are (query, head-in-group) pairs of
+                                    // its kv head (row p: query p / group, head kv * group + p % group)
 };
 
 struct DecodeArgs {

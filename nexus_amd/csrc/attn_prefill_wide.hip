@@ -230,26 +230,34 @@ prefill_wide_kernel(PrefillArgs a)
     const int n = lane & 31, hh = lane >> 5;
     const int rw = wave % L::RWAVES, kg = wave / L::RWAVES;
 
-    // ---- work item: (kv head, query block [heaviest first], q head in group, key split)
-    const int per_kv = a.group * a.n_qblocks * a.n_splits;
+    // ---- work item: (kv head, query block [heaviest first], q head in group, key split).
+    // Packed (short chunks): a block's rows are the (query, head-in-group) pairs p of its kv head
+    // -- query p / group, head kv * group + p % group -- so the group's heads share every K/V tile
+    // and no block is padded to its row count; the item then has no head index.
+    const int heads_per_item = a.pack ? 1 : a.group;
+    const int per_kv = heads_per_item * a.n_qblocks * a.n_splits;
     const int item = xcd_remap_kv(blockIdx.x, a.n_items, a.n_kv_heads, per_kv, a.n_splits);
     const int kvh = item / per_kv;
     int r = item - kvh * per_kv;
-    const int qb = a.n_qblocks - 1 - r / (a.group * a.n_splits);
-    r %= a.group * a.n_splits;
+    const int qb = a.n_qblocks - 1 - r / (heads_per_item * a.n_splits);
+    r %= heads_per_item * a.n_splits;
     const int g = r / a.n_splits;
     const int split = r - g * a.n_splits;
-    const int h = kvh * a.group + g;
+    const int h = kvh * a.group + g;                      // the block's q head (not packed)
+    const int n_rows = a.pack ? a.n_query * a.group : a.n_query;   // rows of the block row space
+    auto row_query = [&](int p) { return a.pack ? p / a.group : p; };
+    auto row_head = [&](int p) { return a.pack ? kvh * a.group + p % a.group : h; };
 
     // ---- key tiles of this workgroup: [t0, t1) of the block's tiles t_lo .. k_hi / BN, split
     // evenly over n_splits workgroups; keys from kmax on belong to later splits (or past the
     // cache end) and are masked.  A sliding window starts the range at the tile of the first
     // row's first key (later rows' earlier keys are masked).
-    const int q0 = qb * BM;
-    const int k_hi = min(a.q_base + min(q0 + BM, a.n_query) - 1, a.n_ctx - 1);
+    const int q0 = qb * BM;                               // first row of the block
+    const int qa = row_query(q0), qz = row_query(min(q0 + BM, n_rows) - 1);   // its first and last query
+    const int k_hi = min(a.q_base + qz, a.n_ctx - 1);
     const int n_tiles = k_hi / BN + 1;
     const bool swa = a.sliding_window > 0;
-    const int t_lo = swa ? min(max(0, a.q_base + q0 + 1 - a.sliding_window) / BN, n_tiles) : 0;
+    const int t_lo = swa ? min(max(0, a.q_base + qa + 1 - a.sliding_window) / BN, n_tiles) : 0;
     const int tps = (n_tiles - t_lo + a.n_splits - 1) / a.n_splits;
     const int t0 = min(t_lo + split * tps, n_tiles), t1 = min(t0 + tps, n_tiles);
     const int kmax = min(a.n_ctx, t1 * BN);
@@ -259,11 +267,12 @@ prefill_wide_kernel(PrefillArgs a)
     // count, no per-wave branches in the loop): tiles past a wave's diagonal are fully masked
     // for it, and key group 1 of an odd tile count takes one tile past t1 (loaded like any
     // other, zero past the cache end, fully masked).
-    const int w_first = q0 + RPW * rw;
-    const bool wave_active = w_first < a.n_query;
+    const int w_first = q0 + RPW * rw;                    // first row of this wave
+    const bool wave_active = w_first < n_rows;
+    const int wq_first = row_query(w_first), wq_last = row_query(w_first + RPW - 1);   // the wave's queries
     int qpos[NB];
 #pragma unroll
-    for (int rb = 0; rb < NB; ++rb) qpos[rb] = a.q_base + w_first + 32 * rb + n;
+    for (int rb = 0; rb < NB; ++rb) qpos[rb] = a.q_base + row_query(w_first + 32 * rb + n);
 
     // ---- K/V staging: thread tid, load j fills LDS bytes 16 * (256 j + tid) of a tile
     const uint32_t kv_bytes = (uint32_t)a.n_ctx * HD * 2;
@@ -332,11 +341,14 @@ prefill_wide_kernel(PrefillArgs a)
     u32x4 qraw[NB][KSTEPS][QV];
     {
         const size_t row_bytes = (size_t)a.n_q_heads * HD * QE;
-        const int blk_rows = min(BM, a.n_query - q0);
-        const rsrc_t qr = make_rsrc_uniform((const char*)a.q + (size_t)q0 * row_bytes, (uint32_t)(blk_rows * row_bytes));
+        const rsrc_t qr = make_rsrc_uniform((const char*)a.q + (size_t)qa * row_bytes, (uint32_t)((qz - qa + 1) * row_bytes));
 #pragma unroll
         for (int rb = 0; rb < NB; ++rb) {
-            const uint32_t qoff = (uint32_t)((RPW * rw + 32 * rb + n) * row_bytes + ((size_t)h * HD + 8 * hh) * QE);
+            // rows past the row space point past the descriptor and read as zero
+            const int p = q0 + RPW * rw + 32 * rb + n;
+            const uint32_t qoff = p < n_rows ? (uint32_t)((size_t)(row_query(p) - qa) * row_bytes +
+                                                          ((size_t)row_head(p) * HD + 8 * hh) * QE)
+                                             : 0x7fffff00u;
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
@@ -479,8 +491,8 @@ prefill_wide_kernel(PrefillArgs a)
     // causal / cache-end / window mask of tile t; wave-uniform test (diagonal and last tiles,
     // and tiles with keys before the window of the wave's last row)
     auto tile_needs_mask = [&](int t) {
-        return t * BN + BN - 1 > a.q_base + w_first || t * BN + BN > kmax ||
-               (swa && t * BN < a.q_base + w_first + RPW - a.sliding_window);
+        return t * BN + BN - 1 > a.q_base + wq_first || t * BN + BN > kmax ||
+               (swa && t * BN < a.q_base + wq_last + 1 - a.sliding_window);
     };
     auto mask_tile = [&](STile& sv, int t) {
         const int key0 = t * BN;
@@ -846,9 +858,10 @@ prefill_wide_kernel(PrefillArgs a)
         // carries the reference's initial max and l = 0.  The combine kernel merges.
 #pragma unroll
         for (int rb = 0; rb < NB; ++rb) {
-            const int qrow = w_first + 32 * rb + n;
-            if (qrow >= a.n_query) continue;
-            const long long prow = (long long)qrow * a.n_q_heads + h, n_all = (long long)a.n_query * a.n_q_heads;
+            const int p = w_first + 32 * rb + n;
+            if (p >= n_rows) continue;
+            const long long prow = (long long)row_query(p) * a.n_q_heads + row_head(p);
+            const long long n_all = (long long)a.n_query * a.n_q_heads;
             float* pr = a.part + part_acc(split, prow, n_all, HD);
 #pragma unroll
             for (int db = 0; db < DBLK; ++db)
@@ -866,10 +879,10 @@ prefill_wide_kernel(PrefillArgs a)
     // lane (row n, hh) holds dims 32 db + 8 a4 + 4 hh + (0..3) of its row
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb) {
-        const int qrow = w_first + 32 * rb + n;
-        if (qrow >= a.n_query) continue;
+        const int p = w_first + 32 * rb + n;
+        if (p >= n_rows) continue;
         const float inv = l_tot[rb] > 0.f ? 1.f / l_tot[rb] : 0.f;
-        const size_t obase = ((size_t)qrow * a.n_q_heads + h) * HD;
+        const size_t obase = ((size_t)row_query(p) * a.n_q_heads + row_head(p)) * HD;
 #pragma unroll
         for (int db = 0; db < DBLK; ++db)
 #pragma unroll

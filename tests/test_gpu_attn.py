@@ -115,6 +115,11 @@ PREFILL_CASES = [
     (16, 2, 256, 16, 9000, 0, True, True, 0, 0.0),       # 4 row groups (2R <= G behind >= 8k keys)
     (40, 8, 128, 24, 17000, 3, False, False, 0, 0.0),    # 4 row groups < G = 5 behind >= 16k, f32 q/o
     (16, 2, 256, 12, 20000, 0, True, False, 300, 20.0),  # window + softcap on that path
+    # chunks of <= 128 queries behind >= 16k keys with packed (query, head-in-group) rows
+    (40, 8, 128, 32, 20000, 0, True, True, 0, 0.0),      # 64-row blocks of 12.8 queries x 5 heads
+    (40, 8, 128, 47, 16500, 2, False, False, 5000, 30.0),  # window + softcap, f32 q/o, ragged last block
+    (16, 2, 256, 128, 17000, 0, True, False, 0, 0.0),    # hd 256: 128-row blocks of 16 queries x 8 heads
+    (24, 4, 192, 100, 16384, 0, False, True, 0, 0.0),    # hd 192, f32 q
 ]
 
 
@@ -192,6 +197,7 @@ GATED_PREFILL_CASES = [
     (8, 1, 256, 64, 4000, True, False, 0, 0.0, True),      # hd 256 in 16 key splits: gate in the row combine
     (6, 2, 192, 70, 2000, False, True, 300, 20.0, True),   # hd 192 key splits, window + softcap
     (8, 2, 128, 80, 0, True, True, 40, 0.0, True),         # window without softcap, 64-row blocks
+    (40, 8, 128, 40, 17000, True, False, 0, 0.0, True),    # packed rows behind a long cache, gated
     (8, 4, 128, 100, 60, False, False, 0, 30.0, True),     # pipelined kernel, softcap
     (8, 2, 128, 256, 3000, True, True, 0, 30.0, True),     # softcapped key split + combine
     (40, 8, 128, 520, 300, True, True, 0, 0.0, True),      # pipelined kernel, 360 64-row blocks
