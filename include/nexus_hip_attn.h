@@ -84,15 +84,30 @@ typedef struct nexus_attn_desc {
  * (src/gpu/vulkan_backend.h:584-608).  The workspace lets the library split a long key
  * range over several workgroups (its size comes from nexus_hip_attn_prefill_ws_bytes();
  * NULL/0, or a smaller one, runs unsplit); split partials are merged by a second launch
- * on the same stream.  A handful of queries (n_query * G <= 32, e.g. speculative verify)
- * runs through the split-KV decode kernels when the workspace allows.  The workspace
- * holds f32 partials only and carries no state between calls (no zeroing needed); calls
- * in flight at once must not share it. */
+ * on the same stream.  Short chunks (n_query * G <= 32, e.g. speculative verify, and a few
+ * more queries behind long caches) run through the split-KV decode kernels when the
+ * workspace allows.  The workspace holds f32 partials only and carries no state between
+ * calls (no zeroing needed); calls in flight at once must not share it. */
 int nexus_hip_attn_prefill(const nexus_attn_desc* desc,
                            const void* q, const uint16_t* k, const uint16_t* v, void* out,
                            void* workspace, size_t workspace_bytes,
                            nexus_stream_t stream);
 size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc);
+
+/* The launch plan nexus_hip_attn_prefill(_gated) follows for `desc` when given
+ * nexus_hip_attn_prefill_ws_bytes() bytes of workspace, on the current device (256 compute
+ * units when no device is visible).  No counterpart in the reference: a diagnostic that lets
+ * tests and tuning check a shape's route without timing it.  Returns NEXUS_OK, or the shape
+ * error nexus_hip_attn_prefill would return for `desc`. */
+enum { NEXUS_PLAN_PREFILL = 0, NEXUS_PLAN_DECODE = 1 };
+typedef struct nexus_attn_prefill_plan {
+    int32_t kernel;      /* NEXUS_PLAN_PREFILL: pipelined prefill kernel; NEXUS_PLAN_DECODE: split-KV decode kernel */
+    int32_t block_rows;  /* rows per workgroup: 64 or 128 (prefill), 16 or 32 (decode)       */
+    int32_t splits;      /* key splits; above 1 a combine launch follows                     */
+    int32_t packed;      /* 1: prefill blocks over the (query, head-in-group) rows of a kv head */
+    int32_t workgroups;  /* workgroups of the attention launch                               */
+} nexus_attn_prefill_plan;
+int nexus_hip_attn_prefill_plan(const nexus_attn_desc* desc, nexus_attn_prefill_plan* plan);
 
 /* Split-KV decode over the cache: n_query >= 1 tokens at positions q_base_pos + i
  * (n_query = 1 is ordinary decode, n_query > 1 is speculative/MTP verify with the

@@ -24,10 +24,14 @@ NEXUS_E_WORKSPACE = -3
 NEXUS_E_LAUNCH = -4
 NEXUS_E_IO = -5
 
+NEXUS_PLAN_PREFILL = 0
+NEXUS_PLAN_DECODE = 1
+
 # Every symbol include/*.h declares (checked by tests/test_capi.py).
 EXPORTED_SYMBOLS = (
     "nexus_hip_attn_prefill",
     "nexus_hip_attn_prefill_ws_bytes",
+    "nexus_hip_attn_prefill_plan",
     "nexus_hip_attn_decode",
     "nexus_hip_attn_decode_ws_bytes",
     "nexus_hip_attn_decode_default_splits",
@@ -89,6 +93,18 @@ PREP_ROPE_INTERLEAVED = 32
 PREP_TRUNC_STORE = 64
 
 
+class PrefillPlan(ctypes.Structure):
+    """struct nexus_attn_prefill_plan (include/nexus_hip_attn.h)."""
+
+    _fields_ = [
+        ("kernel", ctypes.c_int32),
+        ("block_rows", ctypes.c_int32),
+        ("splits", ctypes.c_int32),
+        ("packed", ctypes.c_int32),
+        ("workgroups", ctypes.c_int32),
+    ]
+
+
 class PrepDesc(ctypes.Structure):
     """struct nexus_attn_prep_desc (include/nexus_hip_attn.h)."""
 
@@ -142,6 +158,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.nexus_hip_attn_prefill.restype = ctypes.c_int
     lib.nexus_hip_attn_prefill_ws_bytes.argtypes = [dp]
     lib.nexus_hip_attn_prefill_ws_bytes.restype = sz
+    lib.nexus_hip_attn_prefill_plan.argtypes = [dp, ctypes.POINTER(PrefillPlan)]
+    lib.nexus_hip_attn_prefill_plan.restype = ctypes.c_int
     lib.nexus_hip_attn_decode.argtypes = [dp, vp, vp, vp, vp, vp, ctypes.c_int, vp]
     lib.nexus_hip_attn_decode.restype = ctypes.c_int
     lib.nexus_hip_attn_decode_ws_bytes.argtypes = [dp, ctypes.c_int]
@@ -203,6 +221,16 @@ def _check(rc: int) -> int:
 
 def prefill_ws_bytes(desc: AttnDesc) -> int:
     return int(load().nexus_hip_attn_prefill_ws_bytes(ctypes.byref(desc)))
+
+
+def prefill_plan(desc: AttnDesc) -> dict:
+    """The launch plan of nexus_hip_attn_prefill for `desc` (with its full workspace) on the
+    current device, 256 compute units without one: kernel ("prefill" or "decode"), block_rows,
+    splits, packed, workgroups."""
+    p = PrefillPlan()
+    _check(load().nexus_hip_attn_prefill_plan(ctypes.byref(desc), ctypes.byref(p)))
+    return {"kernel": "decode" if p.kernel == NEXUS_PLAN_DECODE else "prefill", "block_rows": p.block_rows,
+            "splits": p.splits, "packed": bool(p.packed), "workgroups": p.workgroups}
 
 
 def decode_ws_bytes(desc: AttnDesc, n_splits: int = 0) -> int:

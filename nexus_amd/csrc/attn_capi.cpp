@@ -583,6 +583,30 @@ size_t nexus_hip_attn_prefill_ws_bytes(const nexus_attn_desc* desc)
     return prefill_split_ws_bytes(desc, s);
 }
 
+int nexus_hip_attn_prefill_plan(const nexus_attn_desc* desc, nexus_attn_prefill_plan* plan)
+{
+    const int rc = check_desc(desc);
+    if (rc != NEXUS_OK) return rc;
+    if (!plan) return capi_fail(NEXUS_E_INVALID, "null plan pointer");
+    if (small_query_path(desc)) {
+        const int splits = default_decode_splits(desc);
+        plan->kernel = NEXUS_PLAN_DECODE;
+        plan->block_rows = nxa::kDecodeRowTile * decode_row_tiles(desc);
+        plan->splits = splits;
+        plan->packed = 0;
+        plan->workgroups = splits * desc->n_kv_heads * decode_rowgroups(desc);
+        return ok();
+    }
+    const PrefillPlan p = prefill_plan(desc);
+    plan->kernel = NEXUS_PLAN_PREFILL;
+    plan->block_rows = nxa::prefill_wide_rows(p.ks);
+    plan->splits = p.splits;
+    plan->packed = p.pack ? 1 : 0;
+    const long long wgs = prefill_plan_wgs(desc, p);
+    plan->workgroups = wgs > INT_MAX ? INT_MAX : (int)wgs;
+    return ok();
+}
+
 int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, const uint16_t* k,
                                  const uint16_t* v, const float* gate, void* out, void* workspace,
                                  size_t workspace_bytes, nexus_stream_t stream)

@@ -47,7 +47,8 @@ def test_library_has_no_undefined_kernel_symbols():
 
 
 @pytest.mark.parametrize("cls,cname", [(capi.AttnDesc, "nexus_attn_desc"), (capi.PrepDesc, "nexus_attn_prep_desc"),
-                                       (capi.KvLayerView, "nexus_kv_layer_view")])
+                                       (capi.KvLayerView, "nexus_kv_layer_view"),
+                                       (capi.PrefillPlan, "nexus_attn_prefill_plan")])
 def test_desc_layout_matches_header(tmp_path, cls, cname):
     """The ctypes mirrors of the descriptors have the C compiler's size and offsets."""
     import shutil
