@@ -600,7 +600,9 @@ decode_ring_kernel(DecodeArgs a)
 // out[row][d] = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, zeros for a row that
 // saw no key.  One workgroup per (row, 64 dims): thread (split group sg, dim quad dq) folds
 // splits sg, sg + 16, ... of dims 4 dq .. 4 dq + 3 of the slice, eight splits per memory
-// round trip (one round trip up to 128 splits); the 16 split groups merge through LDS.
+// round trip (one round trip up to 128 splits); the 16 split groups merge through LDS.  The
+// partials are read once, with non-temporal loads (measured on MI355X: 4-draft verify at 32k
+// keys, hd 256, 21.5 -> 19.9 us per call; one-token decodes unchanged or slightly faster).
 constexpr int kCombineSliceDims = 64;
 constexpr int kCombineSplitGroups = 16;
 
@@ -625,7 +627,7 @@ combine_slices_kernel(CombineArgs a)
             const int c = c0 + j * SG;
             const bool ok = c < a.n_splits;
             const int cs = ok ? c : 0;
-            x[j] = *(const f32x4*)(a.part + part_acc(cs, row, a.n_rows, HD) + dim);
+            x[j] = __builtin_nontemporal_load((const f32x4*)(a.part + part_acc(cs, row, a.n_rows, HD) + dim));
             ml[j] = *(const f32x2*)(a.part + part_ml(cs, row, a.n_rows, a.n_splits, HD));
             if (!ok) ml[j] = f32x2{kNegBig * 4.f, 0.f};
         }
