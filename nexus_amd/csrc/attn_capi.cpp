@@ -190,12 +190,12 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // Prefill grid of the pipelined kernel (every supported head dim, softcap and sliding window
 // included): 128-row blocks (KS = 1), or 64-row blocks with the key range split over two waves
 // of the workgroup (KS = 2) when 128-row blocks give at most one workgroup per CU (one wave per
-// SIMD), or fewer than two per CU for a chunk at least as long as the cache before it, where
-// causal blocks range up to about twice the mean length and smaller blocks balance better
-// (measured on MI355X, 40 q heads: 1024 queries cold 29.0 -> 23.4 us, 1024 after 1024: 55.7 ->
-// 53.5 us; 32 q heads, 1024 after 2048: 64 -> 55 us; with a longer cache before the chunk
-// 128-row blocks stay faster, 40 q heads, 1024 after 2048/3072/4096/7168: 76/100/124/195 vs
-// 80/107/136/223 us).  Head dims 192 and 256 have the 128-row form only: the two-key-group form does not fit
+// SIMD), or fewer than two per CU for a chunk longer than the cache before it, where causal
+// blocks range up to about twice the mean length and smaller blocks balance better (measured on
+// MI355X with the CU pairing of pair_rotate, 40 q heads: 1024 queries cold 29.7 -> 25.4 us,
+// 36q/4kv 27.6 -> 21.4 us; from a cache as long as the chunk on, 128-row blocks are faster: 40
+// q heads, 1024 after 1024 51.1 vs 53.3 us, 48 q heads 52.3 vs 56.4, head dim 64 31.0 vs 36.6;
+// 1024 after 2048/3072/4096/7168 without the pairing 76/100/124/195 vs 80/107/136/223 us).  Head dims 192 and 256 have the 128-row form only: the two-key-group form does not fit
 // one wave per SIMD's registers.  Either grid splits the key range over workgroups by the rule
 // above.
 // Packed rows: a chunk of at most 128 queries with several q heads per kv head can have its
@@ -225,7 +225,7 @@ PrefillPlan prefill_plan_for(const nexus_attn_desc* d, bool pack)
 {
     PrefillPlan p{1, 1, pack};
     const long long b1 = query_blocks(d, nxa::prefill_wide_rows(1), pack), cus = device_cus();
-    const bool ks2 = b1 <= cus || (b1 < 2 * cus && d->q_base_pos <= d->n_query);
+    const bool ks2 = b1 <= cus || (b1 < 2 * cus && d->q_base_pos < d->n_query);
     p.ks = ks2 && d->head_dim <= 128 ? 2 : 1;
     p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks), pack));
     return p;
@@ -656,6 +656,14 @@ int nexus_hip_attn_prefill_gated(const nexus_attn_desc* desc, const void* q, con
     const long long items = (long long)(plan.pack ? desc->n_kv_heads : desc->n_q_heads) * a.n_qblocks * splits;
     if (items > INT_MAX) return capi_fail(NEXUS_E_UNSUPPORTED, "grid too large");
     a.n_items = (int)items;
+    // a grid between one and two workgroups per CU at two per CU: the CUs that hold two run the
+    // lightest blocks (pair_rotate)
+    const long long cus = device_cus();
+    if (nxa::decode_wg_per_cu(desc->head_dim) == 2 && cus % 8 == 0 && items > cus && items < 2 * cus &&
+        (items - cus) % 8 == 0) {
+        a.pair_rot = (int)((items - cus) / 8);
+        a.pair_span = (int)(cus / 8);
+    }
     const bool q32 = desc->q_dtype == NEXUS_DT_F32, o32 = desc->o_dtype == NEXUS_DT_F32;
     // the softcap form (EXT) only when there is a softcap: a sliding window is masking, which the
     // plain form does too

@@ -283,6 +283,22 @@ __device__ __forceinline__ void wave_lds_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Dispatch position of the workgroup whose item block b runs, for grids of cus < n < 2 cus
+// workgroups at two per CU (cus, n multiples of 8).  The hardware deals block b to XCD b % 8
+// and places the first cus blocks one per CU; block cus + j then lands on the CU of block j
+// (measured on MI355X, every launch alike).  Items are ordered heaviest first per XCD (position
+// t = b / 8 within it), so without this the shared CUs would pair the heaviest blocks with the
+// lightest.  Within each XCD the first-round positions rotate by rot = (n - cus) / 8: positions
+// t < rot (beside an overflow block) take ranks span - rot .. span - 1, the lightest of the first
+// round, and positions rot .. span - 1 (alone on their CU) ranks 0 .. span - rot - 1; overflow
+// positions (t >= span = cus / 8) keep theirs.  A bijection on positions; rot = 0 is identity.
+__device__ __forceinline__ int pair_rotate(int b, int rot, int span)
+{
+    const int x = b & 7, t = b >> 3;
+    if (rot <= 0 || t >= span) return b;
+    return x + 8 * (t < rot ? t + span - rot : t - rot);
+}
+
 // Map a linear block index to a work item so that each XCD (blocks are dealt round-robin
 // over the 8 XCDs) receives one contiguous range of items: items that share a KV head
 // then share that XCD's L2.

@@ -41,6 +41,7 @@ struct PrefillArgs {
     int n_qblocks, n_splits, n_items;
     int pack;                       // non-zero: a block's rows are (query, head-in-group) pairs of
                                     // its kv head (row p: query p / group, head kv * group + p % group)
+    int pair_rot, pair_span;        // pair_rotate() of the dispatch position (0, 0: none)
 };
 
 struct DecodeArgs {

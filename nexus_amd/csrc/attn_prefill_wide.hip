@@ -236,7 +236,7 @@ prefill_wide_kernel(PrefillArgs a)
     // and no block is padded to its row count; the item then has no head index.
     const int heads_per_item = a.pack ? 1 : a.group;
     const int per_kv = heads_per_item * a.n_qblocks * a.n_splits;
-    const int item = xcd_remap_kv(blockIdx.x, a.n_items, a.n_kv_heads, per_kv, a.n_splits);
+    const int item = xcd_remap_kv(pair_rotate(blockIdx.x, a.pair_rot, a.pair_span), a.n_items, a.n_kv_heads, per_kv, a.n_splits);
     const int kvh = item / per_kv;
     int r = item - kvh * per_kv;
     const int qb = a.n_qblocks - 1 - r / (heads_per_item * a.n_splits);

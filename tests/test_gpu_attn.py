@@ -111,7 +111,7 @@ PREFILL_CASES = [
     (18, 6, 64, 1000, 50, 0, True, True, 0, 0.0),        # 6 kv heads: 2 groups of 3 on 4 XCDs each
     (15, 3, 256, 600, 0, 0, True, False, 0, 0.0),        # 3 kv heads, hd 256: one group on 8 XCDs
     (16, 2, 256, 1024, 1024, 0, True, True, 0, 0.0),     # the engine's 1024-token tile at hd 256: 128 blocks in 2 splits
-    (40, 8, 128, 1024, 1024, 0, True, True, 0, 0.0),     # its second tile at 40 heads: 64-row blocks (chunk = cache)
+    (40, 8, 128, 1024, 1024, 0, True, True, 0, 0.0),     # its second tile at 40 heads: 320 blocks, paired CUs rotated
     # short chunks over long caches through the split-KV decode kernel (several 32-row groups)
     (16, 2, 256, 16, 9000, 0, True, True, 0, 0.0),       # 4 row groups (2R <= G behind >= 8k keys)
     (40, 8, 128, 24, 17000, 3, False, False, 0, 0.0),    # 4 row groups < G = 5 behind >= 16k, f32 q/o

@@ -110,7 +110,7 @@ def _plain_wgs(hq, hkv, hd, nq, base):
     ((16, 2, 256, 1024, 1024), P(128, 2, 256)),       # the engine's 1024-token tile at hd 256
     ((8, 2, 128, 256, 3000), P(64, 8, 256)),          # short chunk over a longer cache: key splits
     ((40, 8, 128, 1024, 0), P(64, 1, 640)),           # the engine's first 1024-token tile: 64 rows
-    ((40, 8, 128, 1024, 1024), P(64, 1, 640)),        # ... and its second (chunk as long as the cache)
+    ((40, 8, 128, 1024, 1024), P(128, 1, 320)),       # its second (cache as long as the chunk): 128 rows
     ((40, 8, 128, 1024, 2048), P(128, 1, 320)),       # a longer cache before the chunk: 128 rows
 ])
 def test_block_rows_and_splits(shape, want):
