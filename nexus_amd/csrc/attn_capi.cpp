@@ -202,11 +202,12 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // blocks over the (query, head-in-group) pairs of each kv head instead of one padded block per q
 // head, so the group's heads share every K/V tile (read once per block, not once per q head) and
 // only the last block of a kv head is partly filled.  It pays behind long caches, where the
-// unpacked grid's G-fold K/V reads dominate, and is taken there (>= 16k keys) when its grid is at
-// least as large as the unpacked one or fills every CU (fewer blocks, so a smaller grid).
+// unpacked grid's G-fold K/V reads dominate, and is taken there (>= 16k keys) when its grid has at
+// least 3/4 of the workgroups of the unpacked one or of the CUs (fewer blocks, so a smaller grid).
 // Measured on MI355X: 40q/8kv hd 128, 32/48/96 queries over 32k keys 90/92/160 -> 63/76/128 us;
-// behind 4-8k keys within +-10% either way; 16q/2kv hd 256, 32 queries over 8k packed into 64
-// workgroups instead of 256: 14% slower.
+// 64q/8kv, 40 queries over 32k (240 packed workgroups against 256) 129 -> 93 us; behind 4-8k keys
+// within +-10% either way; 16q/2kv hd 256, 32 queries over 8k packed into 64 workgroups instead
+// of 256: 14% slower.
 struct PrefillPlan {
     int ks;
     int splits;
@@ -241,23 +242,27 @@ PrefillPlan prefill_plan(const nexus_attn_desc* d)
     const PrefillPlan plain = prefill_plan_for(d, false);
     if (d->n_query > 128 || d->n_q_heads == d->n_kv_heads || d->n_ctx < 16384) return plain;
     const PrefillPlan packed = prefill_plan_for(d, true);
-    return prefill_plan_wgs(d, packed) >= std::min<long long>(prefill_plan_wgs(d, plain), device_cus()) ? packed : plain;
+    return 4 * prefill_plan_wgs(d, packed) >= 3 * std::min<long long>(prefill_plan_wgs(d, plain), device_cus()) ? packed : plain;
 }
 
 // Chunks short enough for the split-KV decode kernel.  It streams a kv head's K/V once per group
-// of 32 (query, head-in-group) rows (R groups), where the prefill kernel reads it once per q head
-// (G times) into 128-query blocks such a chunk barely fills.  Measured on MI355X (8-64 queries):
-// the decode kernel wins for one group at any length, while 2R <= G behind >= 8k keys (16q/2kv hd
-// 256, 16 queries over 8k: 22.8 vs 27.7 us) and while R < G behind >= 16k (8 queries over 32k: 29.7
-// vs 77.0 us; 40q/8kv hd 128, 24 over 32k: 66 vs 92); otherwise the prefill kernel's lower fixed
-// costs win (40q/8kv hd 128, 12 queries over 4k: 14.6 vs 16.2 us).
+// of 32 (query, head-in-group) rows (R groups), where the unpacked prefill kernel reads it once
+// per q head (G times) into 128-query blocks such a chunk barely fills, and the packed one once
+// per 64 or 128 rows.  Measured on MI355X (8-64 queries): the decode kernel wins for one group at
+// any length, while 2R <= G behind 8k-16k keys (16q/2kv hd 256, 16 queries over 8k: 22.8 vs 27.7
+// us; 64q/8kv hd 128, 8 queries over 12k: 20.9 vs 37.2) and, behind >= 16k keys, at head dims 192
+// and 256 while R < G (8 queries over 32k: 29.7 vs 77.0 us; 24q/4kv hd 192, 24 queries: 79 vs 95),
+// at head dims <= 128 for R <= 2 (ties with packed rows); from R = 3 the packed prefill wins there
+// (64q/8kv hd 128, 24 queries over 17k/32k: 52/94 -> 34/64 us; 40q/8kv, 25 queries: 37/61 ->
+// 27/49 us).  Otherwise the prefill kernel's lower fixed costs win (40q/8kv hd 128, 12 queries
+// over 4k: 14.6 vs 16.2 us).
 bool small_query_path(const nexus_attn_desc* d)
 {
     const long long per = (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
     const long long groups = (decode_rows(d) + per - 1) / per;
     const long long g = d->n_q_heads / d->n_kv_heads;
     if (groups <= 1) return true;
-    if (d->n_ctx >= 16384 && groups < g) return true;
+    if (d->n_ctx >= 16384) return groups < g && (d->head_dim > 128 || groups <= 2);
     return d->n_ctx >= 8192 && 2 * groups <= g;
 }
 

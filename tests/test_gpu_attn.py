@@ -114,13 +114,16 @@ PREFILL_CASES = [
     (40, 8, 128, 1024, 1024, 0, True, True, 0, 0.0),     # its second tile at 40 heads: 320 blocks, paired CUs rotated
     # short chunks over long caches through the split-KV decode kernel (several 32-row groups)
     (16, 2, 256, 16, 9000, 0, True, True, 0, 0.0),       # 4 row groups (2R <= G behind >= 8k keys)
-    (40, 8, 128, 24, 17000, 3, False, False, 0, 0.0),    # 4 row groups < G = 5 behind >= 16k, f32 q/o
+    (40, 8, 128, 12, 17000, 3, False, False, 0, 0.0),    # 2 row groups at hd 128 behind >= 16k, f32 q/o
+    (64, 8, 128, 8, 12000, 0, True, True, 0, 0.0),       # 2R <= G = 8 behind 8k-16k keys
     (16, 2, 256, 12, 20000, 0, True, False, 300, 20.0),  # window + softcap on that path
     # chunks of <= 128 queries behind >= 16k keys with packed (query, head-in-group) rows
     (40, 8, 128, 32, 20000, 0, True, True, 0, 0.0),      # 64-row blocks of 12.8 queries x 5 heads
     (40, 8, 128, 47, 16500, 2, False, False, 5000, 30.0),  # window + softcap, f32 q/o, ragged last block
     (16, 2, 256, 128, 17000, 0, True, False, 0, 0.0),    # hd 256: 128-row blocks of 16 queries x 8 heads
     (24, 4, 192, 100, 16384, 0, False, True, 0, 0.0),    # hd 192, f32 q
+    (40, 8, 128, 24, 17000, 3, False, False, 0, 0.0),    # 4 row groups at hd 128: packed, f32 q/o
+    (64, 8, 128, 20, 17000, 0, True, True, 0, 0.0),      # G = 8: 240 packed workgroups against 256 plain
 ]
 
 

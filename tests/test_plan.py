@@ -54,11 +54,19 @@ def test_bench_shapes(shape, want):
     ((16, 2, 256, 16, 9000), "decode"),               # R = 4
     ((16, 2, 256, 16, 8000), "prefill"),              # below 8k keys
     ((16, 2, 256, 20, 9000), "prefill"),              # R = 5: 2R > G, and below 16k
-    # R < G behind >= 16k keys
+    # behind >= 16k keys: R < G at head dims 192/256, R <= 2 at head dims <= 128 (packed rows beyond)
     ((16, 2, 256, 24, 17000), "decode"),              # R = 6 < 8
     ((16, 2, 256, 32, 17000), "prefill"),             # R = 8 = G
-    ((40, 8, 128, 24, 17000), "decode"),              # R = 4 < G = 5
+    ((24, 4, 192, 24, 32768), "decode"),              # R = 5 < 6
+    ((40, 8, 128, 12, 17000), "decode"),              # R = 2 at head dim 128
+    ((40, 8, 128, 24, 17000), "prefill"),             # R = 4 at head dim 128: packed rows
+    ((64, 8, 128, 16, 32768), "prefill"),             # R = 4 < G = 8 at head dim 128: packed rows
     ((40, 8, 128, 32, 17000), "prefill"),             # R = 5 = G
+    ((16, 8, 128, 24, 32768), "prefill"),             # R = 2 = G: nothing shared
+    # 2R <= G behind 8k-16k keys at any head dim
+    ((64, 8, 128, 8, 12000), "decode"),
+    ((64, 8, 128, 16, 12000), "decode"),
+    ((64, 8, 128, 20, 12000), "prefill"),             # 2R = 10 > 8
     ((40, 8, 128, 12, 4000), "prefill"),              # short cache: the prefill kernel's lower fixed costs
     # window + softcap ride the same rule
     ((16, 2, 256, 12, 20000, 300, 20.0), "decode"),
@@ -73,6 +81,8 @@ def test_short_chunk_route(shape, kernel):
     ((16, 2, 256, 128, 17000), True),
     ((24, 4, 192, 100, 16384), True),
     ((40, 8, 128, 40, 17000), True),                  # the gated packed case
+    ((64, 8, 128, 20, 17000), True),                  # 240 packed workgroups against 256 plain ones
+    ((64, 8, 128, 40, 32768), True),
     ((40, 8, 128, 32, 16000), False),                 # n_ctx below 16k
     ((16, 2, 256, 32, 8192), False),                  # packing lost there (64 workgroups for 256)
     ((40, 8, 128, 160, 32768), False),                # more than 128 queries
@@ -85,15 +95,15 @@ def test_packed_rows_rule(shape, packed):
 
 
 def test_packed_grid_never_smaller_than_it_needs():
-    """Packing is taken only when its grid is at least as large as the plain one or fills
-    every CU."""
+    """Packing is taken only when its grid has at least 3/4 of the workgroups of the plain one
+    or of the CUs."""
     for hq, hkv in [(40, 8), (16, 2), (24, 4), (32, 8), (64, 8)]:
         for hd in (64, 128, 192, 256):
             for nq in (33, 48, 64, 96, 100, 128):
                 for base in (16384, 32768, 65536):
                     p = plan(hq, hkv, hd, nq, base)
                     if p["packed"]:
-                        assert p["workgroups"] >= 256 or p["workgroups"] >= _plain_wgs(hq, hkv, hd, nq, base), \
+                        assert 4 * p["workgroups"] >= 3 * min(256, _plain_wgs(hq, hkv, hd, nq, base)), \
                             (hq, hkv, hd, nq, base, p)
 
 
