@@ -202,12 +202,15 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // blocks over the (query, head-in-group) pairs of each kv head instead of one padded block per q
 // head, so the group's heads share every K/V tile (read once per block, not once per q head) and
 // only the last block of a kv head is partly filled.  It pays behind long caches, where the
-// unpacked grid's G-fold K/V reads dominate, and is taken there (>= 16k keys) when its grid has at
-// least 3/4 of the workgroups of the unpacked one or of the CUs (fewer blocks, so a smaller grid).
-// Measured on MI355X: 40q/8kv hd 128, 32/48/96 queries over 32k keys 90/92/160 -> 63/76/128 us;
-// 64q/8kv, 40 queries over 32k (240 packed workgroups against 256) 129 -> 93 us; behind 4-8k keys
-// within +-10% either way; 16q/2kv hd 256, 32 queries over 8k packed into 64 workgroups instead
-// of 256: 14% slower.
+// unpacked grid's G-fold K/V reads dominate: taken behind >= 8k keys at head dims >= 128 (>= 16k
+// at 64) when it has fewer blocks than the unpacked grid and its grid keeps at least 3/4 of the
+// workgroups of the unpacked one or of the CUs.  Measured on MI355X: 40q/8kv hd 128, 32/48/96
+// queries over 32k keys 90/92/160 -> 63/76/128 us, 24 over 9k 25.7 -> 18.1 us; 64q/8kv, 20
+// queries over 12k 39.3 -> 23.5 us, 40 over 32k (240 packed workgroups against 256) 129 -> 93
+// us; 24q/4kv hd 192, 48 queries over 12k 42.7 -> 34.7 us; as many blocks either way (40q/8kv, 64
+// queries) or head dim 64 behind 9k keys: 1-7% slower packed; behind 4-6k keys within +-10%
+// either way; 16q/2kv hd 256, 32 queries over 8k packed into 64 workgroups instead of 256: 14%
+// slower.
 struct PrefillPlan {
     int ks;
     int splits;
@@ -240,8 +243,12 @@ long long prefill_plan_wgs(const nexus_attn_desc* d, const PrefillPlan& p)
 PrefillPlan prefill_plan(const nexus_attn_desc* d)
 {
     const PrefillPlan plain = prefill_plan_for(d, false);
-    if (d->n_query > 128 || d->n_q_heads == d->n_kv_heads || d->n_ctx < 16384) return plain;
+    if (d->n_query > 128 || d->n_q_heads == d->n_kv_heads || d->n_ctx < (d->head_dim >= 128 ? 8192 : 16384))
+        return plain;
     const PrefillPlan packed = prefill_plan_for(d, true);
+    // packing must save K/V reads (fewer blocks) and keep the grid at 3/4 of the plain one or of the CUs
+    if (query_blocks(d, nxa::prefill_wide_rows(packed.ks), true) >= query_blocks(d, nxa::prefill_wide_rows(plain.ks), false))
+        return plain;
     return 4 * prefill_plan_wgs(d, packed) >= 3 * std::min<long long>(prefill_plan_wgs(d, plain), device_cus()) ? packed : plain;
 }
 

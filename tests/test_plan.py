@@ -78,12 +78,16 @@ def test_short_chunk_route(shape, kernel):
 @pytest.mark.parametrize("shape,packed", [
     ((40, 8, 128, 32, 20000), True),
     ((40, 8, 128, 47, 16500, 5000, 30.0), True),
-    ((16, 2, 256, 128, 17000), True),
+    ((16, 2, 256, 96, 17000), True),                  # 12 packed 128-row blocks against 16
+    ((16, 2, 256, 128, 17000), False),                # 16 blocks either way: nothing saved
     ((24, 4, 192, 100, 16384), True),
     ((40, 8, 128, 40, 17000), True),                  # the gated packed case
     ((64, 8, 128, 20, 17000), True),                  # 240 packed workgroups against 256 plain ones
     ((64, 8, 128, 40, 32768), True),
-    ((40, 8, 128, 32, 16000), False),                 # n_ctx below 16k
+    ((40, 8, 128, 24, 9000), True),                   # 8k-16k keys at head dim 128
+    ((40, 8, 128, 32, 7000), False),                  # below 8k keys
+    ((32, 8, 64, 48, 9000), False),                   # head dim 64 below 16k keys
+    ((40, 8, 128, 64, 9000), False),                  # 40 blocks either way
     ((16, 2, 256, 32, 8192), False),                  # packing lost there (64 workgroups for 256)
     ((40, 8, 128, 160, 32768), False),                # more than 128 queries
     ((8, 8, 128, 64, 20000), False),                  # no GQA group to pack
