@@ -173,7 +173,10 @@ size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
 // splits take 96 us against 62 unsplit).  Below half a workgroup per CU (head dims <= 128, two
 // workgroups per CU), or below one workgroup per CU (head dims 192 and 256, one per CU: a
 // 1024-token prompt tile of 16 heads is 128 workgroups, which left half the CUs idle), split so
-// the grid reaches about one workgroup per CU, each split keeping >= 4 key tiles of 64.
+// the grid reaches about one workgroup per CU, each split keeping >= 4 key tiles of 64, up to 64
+// splits: grids of a few blocks behind long caches need them to fill the chip (measured on
+// MI355X, 16q/2kv hd 256 behind 32k keys, 32/48 queries at most 16 splits 76/80 us, 64 splits
+// 43/52 us; 24q/4kv hd 192, 32 queries 93 -> 49 us; 4-head MHA, 64 queries 34 -> 21 us).
 int prefill_splits(const nexus_attn_desc* d, long long base)
 {
     const long long cus = device_cus();
@@ -183,7 +186,7 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
     key_range(d, &kb, &ke);
     const long long tiles = (ke - kb + 63) / 64;
     if (s > tiles / 4) s = tiles / 4;
-    if (s > 16) s = 16;
+    if (s > 64) s = 64;
     return s < 1 ? 1 : (int)s;
 }
 
@@ -257,19 +260,20 @@ PrefillPlan prefill_plan(const nexus_attn_desc* d)
 // per q head (G times) into 128-query blocks such a chunk barely fills, and the packed one once
 // per 64 or 128 rows.  Measured on MI355X (8-64 queries): the decode kernel wins for one group at
 // any length, while 2R <= G behind 8k-16k keys (16q/2kv hd 256, 16 queries over 8k: 22.8 vs 27.7
-// us; 64q/8kv hd 128, 8 queries over 12k: 20.9 vs 37.2) and, behind >= 16k keys, at head dims 192
-// and 256 while R < G (8 queries over 32k: 29.7 vs 77.0 us; 24q/4kv hd 192, 24 queries: 79 vs 95),
-// at head dims <= 128 for R <= 2 (ties with packed rows); from R = 3 the packed prefill wins there
-// (64q/8kv hd 128, 24 queries over 17k/32k: 52/94 -> 34/64 us; 40q/8kv, 25 queries: 37/61 ->
-// 27/49 us).  Otherwise the prefill kernel's lower fixed costs win (40q/8kv hd 128, 12 queries
-// over 4k: 14.6 vs 16.2 us).
+// us; 64q/8kv hd 128, 8 queries over 12k: 20.9 vs 37.2) and, behind >= 16k keys, while R < G and
+// either R <= 2 (ties with packed rows) or the chunk does not pack into a full grid (16q/2kv hd
+// 256, 12-16 queries over 17k: 24-28 us against 44-46 on the unpacked prefill kernel).  From R = 3
+// packed rows win where they fill the grid: 64q/8kv hd 128, 24 queries over 17k/32k 52/94 -> 34/64
+// us; 40q/8kv, 25 queries 37/61 -> 27/49 us; 16q/2kv hd 256, 24 queries 39/63 -> 33/40 us; 24q/4kv
+// hd 192, 16/24 queries over 32k 51/80 -> 35/48 us.  Otherwise the prefill kernel's lower fixed
+// costs win (40q/8kv hd 128, 12 queries over 4k: 14.6 vs 16.2 us).
 bool small_query_path(const nexus_attn_desc* d)
 {
     const long long per = (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
     const long long groups = (decode_rows(d) + per - 1) / per;
     const long long g = d->n_q_heads / d->n_kv_heads;
     if (groups <= 1) return true;
-    if (d->n_ctx >= 16384) return groups < g && (d->head_dim > 128 || groups <= 2);
+    if (d->n_ctx >= 16384) return groups < g && (groups <= 2 || !prefill_plan(d).pack);
     return d->n_ctx >= 8192 && 2 * groups <= g;
 }
 

@@ -122,6 +122,11 @@ PREFILL_CASES = [
     (40, 8, 128, 47, 16500, 2, False, False, 5000, 30.0),  # window + softcap, f32 q/o, ragged last block
     (16, 2, 256, 96, 17000, 0, True, False, 0, 0.0),     # hd 256: 12 packed 128-row blocks of 16 queries x 8 heads
     (64, 8, 128, 20, 12000, 0, True, True, 0, 0.0),      # packed behind 8k-16k keys
+    (16, 2, 256, 32, 17000, 0, True, True, 0, 0.0),      # 4 packed blocks in 64 key splits
+    (4, 4, 128, 64, 20000, 0, False, False, 0, 0.0),     # MHA, 4 blocks in 64 key splits, f32 q/o
+    (8, 1, 128, 32, 20000, 0, True, False, 0, 0.0),      # one kv head: packed, 64 splits
+    (24, 4, 192, 16, 20000, 0, True, True, 0, 0.0),      # R = 3 < G = 6: packed rather than the decode kernel
+    (8, 1, 256, 16, 20000, 0, False, False, 0, 0.0),     # R = 4 < G = 8 that cannot pack: decode kernel
     (24, 4, 192, 100, 16384, 0, False, True, 0, 0.0),    # hd 192, f32 q
     (40, 8, 128, 24, 17000, 3, False, False, 0, 0.0),    # 4 row groups at hd 128: packed, f32 q/o
     (64, 8, 128, 20, 17000, 0, True, True, 0, 0.0),      # G = 8: 240 packed workgroups against 256 plain

@@ -54,10 +54,13 @@ def test_bench_shapes(shape, want):
     ((16, 2, 256, 16, 9000), "decode"),               # R = 4
     ((16, 2, 256, 16, 8000), "prefill"),              # below 8k keys
     ((16, 2, 256, 20, 9000), "prefill"),              # R = 5: 2R > G, and below 16k
-    # behind >= 16k keys: R < G at head dims 192/256, R <= 2 at head dims <= 128 (packed rows beyond)
-    ((16, 2, 256, 24, 17000), "decode"),              # R = 6 < 8
+    # behind >= 16k keys: R < G, and R <= 2 or no packed grid that fills the chip
+    ((16, 2, 256, 8, 17000), "decode"),               # R = 2
+    ((16, 2, 256, 16, 17000), "decode"),              # R = 4: one packed block per kv head, too small a grid
+    ((16, 2, 256, 24, 17000), "prefill"),             # R = 6 < 8, but 4 packed blocks fill the grid
     ((16, 2, 256, 32, 17000), "prefill"),             # R = 8 = G
-    ((24, 4, 192, 24, 32768), "decode"),              # R = 5 < 6
+    ((24, 4, 192, 24, 32768), "prefill"),             # R = 5 < 6, packed
+    ((8, 1, 128, 16, 32768), "decode"),               # R = 4, one kv head: packing cannot fill the grid
     ((40, 8, 128, 12, 17000), "decode"),              # R = 2 at head dim 128
     ((40, 8, 128, 24, 17000), "prefill"),             # R = 4 at head dim 128: packed rows
     ((64, 8, 128, 16, 32768), "prefill"),             # R = 4 < G = 8 at head dim 128: packed rows
@@ -123,6 +126,8 @@ def _plain_wgs(hq, hkv, hd, nq, base):
     ((40, 8, 128, 520, 300), P(64, 1, 360)),          # 360 64-row blocks
     ((16, 2, 256, 1024, 1024), P(128, 2, 256)),       # the engine's 1024-token tile at hd 256
     ((8, 2, 128, 256, 3000), P(64, 8, 256)),          # short chunk over a longer cache: key splits
+    ((4, 4, 128, 64, 32768), P(64, 64, 256)),         # 4 blocks behind 32k keys: 64 splits
+    ((16, 2, 256, 32, 32768), P(128, 64, 256, True)), # 4 packed blocks, 64 splits
     ((40, 8, 128, 1024, 0), P(64, 1, 640)),           # the engine's first 1024-token tile: 64 rows
     ((40, 8, 128, 1024, 1024), P(128, 1, 320)),       # its second (cache as long as the chunk): 128 rows
     ((40, 8, 128, 1024, 2048), P(128, 1, 320)),       # a longer cache before the chunk: 128 rows
