@@ -116,6 +116,7 @@ PREFILL_CASES = [
     (16, 2, 256, 16, 9000, 0, True, True, 0, 0.0),       # 4 row groups (2R <= G behind >= 8k keys)
     (40, 8, 128, 12, 17000, 3, False, False, 0, 0.0),    # 2 row groups at hd 128 behind >= 16k, f32 q/o
     (64, 8, 128, 8, 12000, 0, True, True, 0, 0.0),       # 2R <= G = 8 behind 8k-16k keys
+    (48, 8, 128, 16, 9000, 0, True, True, 0, 0.0),       # R = 3, 2R <= G: packed rather than the decode kernel
     (16, 2, 256, 12, 20000, 0, True, False, 300, 20.0),  # window + softcap on that path
     # chunks of <= 128 queries behind >= 16k keys with packed (query, head-in-group) rows
     (40, 8, 128, 32, 20000, 0, True, True, 0, 0.0),      # 64-row blocks of 12.8 queries x 5 heads

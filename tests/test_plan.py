@@ -66,9 +66,10 @@ def test_bench_shapes(shape, want):
     ((64, 8, 128, 16, 32768), "prefill"),             # R = 4 < G = 8 at head dim 128: packed rows
     ((40, 8, 128, 32, 17000), "prefill"),             # R = 5 = G
     ((16, 8, 128, 24, 32768), "prefill"),             # R = 2 = G: nothing shared
-    # 2R <= G behind 8k-16k keys at any head dim
-    ((64, 8, 128, 8, 12000), "decode"),
-    ((64, 8, 128, 16, 12000), "decode"),
+    # 2R <= G behind 8k-16k keys, again R <= 2 or no packed grid
+    ((64, 8, 128, 8, 12000), "decode"),               # R = 2
+    ((64, 8, 128, 16, 12000), "prefill"),             # R = 4: packed
+    ((16, 2, 256, 16, 9000), "decode"),               # R = 4: too few packed blocks
     ((64, 8, 128, 20, 12000), "prefill"),             # 2R = 10 > 8
     ((40, 8, 128, 12, 4000), "prefill"),              # short cache: the prefill kernel's lower fixed costs
     # window + softcap ride the same rule
