@@ -167,24 +167,27 @@ size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
 }
 
 // Split count of a prefill grid of `base` query-block workgroups.  Splitting costs a partial
-// write + read per row and split plus a combine launch, which only pays off when the unsplit
-// grid leaves most CUs idle (measured on MI355X: 160 workgroups of 512 queries x 40 heads run
-// faster unsplit than in 3 splits; 320 pipelined workgroups of 64 queries x 40 heads in 2
-// splits take 96 us against 62 unsplit).  Below half a workgroup per CU (head dims <= 128, two
-// workgroups per CU), or below one workgroup per CU (head dims 192 and 256, one per CU: a
-// 1024-token prompt tile of 16 heads is 128 workgroups, which left half the CUs idle), split so
-// the grid reaches about one workgroup per CU, each split keeping >= 4 key tiles of 64, up to 64
-// splits: grids of a few blocks behind long caches need them to fill the chip (measured on
-// MI355X, 16q/2kv hd 256 behind 32k keys, 32/48 queries at most 16 splits 76/80 us, 64 splits
-// 43/52 us; 24q/4kv hd 192, 32 queries 93 -> 49 us; 4-head MHA, 64 queries 34 -> 21 us).
+// write + read per row and split plus a combine launch, so a grid of at least one workgroup per
+// CU stays whole (320 pipelined workgroups of 64 queries x 40 heads in 2 splits took 96 us
+// against 62 unsplit).  Below that the key range is split so the grid reaches about one
+// workgroup per CU, or two at head dims <= 128 (two resident per CU; a workgroup alone on its CU
+// runs one wave per SIMD) while each split keeps >= 16 key tiles of 64; always >= 4 tiles per
+// split and at most 64 splits.  Measured on MI355X: 40q/8kv hd 128, 200/256 queries over 32k
+// keys in 160 workgroups 432/427 us, split three ways 192/204 us; 32q/8kv, 256 over 16k (128
+// workgroups) 187 -> 90 us; 32/48/64 queries over 32k at one workgroup per CU 61/75/89 us, at two
+// 48/54/62 us; 24 over 9k (9 tiles per split at one per CU) 18 us, at two 24 us; 16q/2kv hd 256
+// behind 32k keys, 32/48 queries at most 16 splits 76/80 us, 64 splits 43/52 us; 24q/4kv hd 192,
+// 32 queries 93 -> 49 us; 4-head MHA, 64 queries 34 -> 21 us.
 int prefill_splits(const nexus_attn_desc* d, long long base)
 {
     const long long cus = device_cus();
-    if ((nxa::decode_wg_per_cu(d->head_dim) == 2 ? 2 * base : base) >= cus) return 1;
-    long long s = cus / base;
+    if (base >= cus) return 1;
     int kb, ke;
     key_range(d, &kb, &ke);
     const long long tiles = (ke - kb + 63) / 64;
+    long long s = cus / base;                                  // about one workgroup per CU
+    if (nxa::decode_wg_per_cu(d->head_dim) == 2 && tiles * base >= 16LL * 2 * cus)
+        s = 2 * cus / base;                                    // two, while splits keep >= 16 tiles
     if (s > tiles / 4) s = tiles / 4;
     if (s > 64) s = 64;
     return s < 1 ? 1 : (int)s;

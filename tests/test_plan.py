@@ -128,6 +128,10 @@ def _plain_wgs(hq, hkv, hd, nq, base):
     ((16, 2, 256, 1024, 1024), P(128, 2, 256)),       # the engine's 1024-token tile at hd 256
     ((8, 2, 128, 256, 3000), P(64, 8, 256)),          # short chunk over a longer cache: key splits
     ((4, 4, 128, 64, 32768), P(64, 64, 256)),         # 4 blocks behind 32k keys: 64 splits
+    ((40, 8, 128, 256, 32768), P(64, 3, 480)),        # 160 blocks: split toward two per CU
+    ((32, 8, 128, 256, 16384), P(64, 4, 512)),        # 128 blocks
+    ((40, 8, 128, 64, 32768), P(64, 12, 480)),        # 40 blocks, 43 tiles per split at two per CU
+    ((40, 8, 128, 24, 9000), P(64, 16, 256, True)),   # 16 packed blocks, too few tiles for two per CU
     ((16, 2, 256, 32, 32768), P(128, 64, 256, True)), # 4 packed blocks, 64 splits
     ((40, 8, 128, 1024, 0), P(64, 1, 640)),           # the engine's first 1024-token tile: 64 rows
     ((40, 8, 128, 1024, 1024), P(128, 1, 320)),       # its second (cache as long as the chunk): 128 rows
