@@ -265,11 +265,12 @@ PrefillPlan prefill_plan(const nexus_attn_desc* d)
 // any length, and against the unpacked prefill kernel while 2R <= G behind 8k-16k keys (16q/2kv
 // hd 256, 16 queries over 8k: 22.8 vs 27.7 us; 64q/8kv hd 128, 8 queries over 12k: 20.9 vs 37.2)
 // or R < G behind >= 16k (16q/2kv hd 256, 12-16 queries over 17k: 24-28 vs 44-46 us).  Packed rows
-// tie with it at R <= 2 and win from R = 3 wherever they fill the grid: 64q/8kv hd 128, 12/16
-// queries over 12k 28/31 -> 20/21 us, 24 over 17k/32k 52/94 -> 34/64 us; 40q/8kv, 25 queries over
-// 17k/32k 37/61 -> 27/49 us; 16q/2kv hd 256, 24 queries 39/63 -> 33/40 us; 24q/4kv hd 192, 12
-// queries over 12k 25 -> 21 us, 16/24 over 32k 51/80 -> 35/48 us.  Otherwise the prefill
-// kernel's lower fixed costs win (40q/8kv hd 128, 12 queries over 4k: 14.6 vs 16.2 us).
+// beat it wherever they fill the grid (R = 2: 40q/8kv hd 128, 12 queries over 17k/32k 27/44 ->
+// 23/37 us, 32q/8kv hd 64, 16 over 32k 31 -> 21 us, 40q/8kv, 8 over 64k 77 -> 59 us; R >= 3:
+// 64q/8kv, 12/16 queries over 12k 28/31 -> 20/21 us, 24 over 17k/32k 52/94 -> 34/64 us; 16q/2kv hd
+// 256, 24 queries 39/63 -> 33/40 us; 24q/4kv hd 192, 16/24 over 32k 51/80 -> 35/48 us), so the
+// decode kernel keeps the chunks that do not pack.  Otherwise the prefill kernel's lower fixed
+// costs win (40q/8kv hd 128, 12 queries over 4k: 14.6 vs 16.2 us).
 bool small_query_path(const nexus_attn_desc* d)
 {
     const long long per = (long long)nxa::kDecodeRowTile * nxa::kDecodeMaxRowTiles;
@@ -277,7 +278,7 @@ bool small_query_path(const nexus_attn_desc* d)
     const long long g = d->n_q_heads / d->n_kv_heads;
     if (groups <= 1) return true;
     const bool fewer = d->n_ctx >= 16384 ? groups < g : (d->n_ctx >= 8192 && 2 * groups <= g);
-    return fewer && (groups <= 2 || !prefill_plan(d).pack);
+    return fewer && !prefill_plan(d).pack;
 }
 
 int launch_combine_for(const nexus_attn_desc* d, float* ws, void* out, const float* gate, int n_splits,

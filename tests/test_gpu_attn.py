@@ -114,8 +114,9 @@ PREFILL_CASES = [
     (40, 8, 128, 1024, 1024, 0, True, True, 0, 0.0),     # its second tile at 40 heads: 320 blocks, paired CUs rotated
     # short chunks over long caches through the split-KV decode kernel (several 32-row groups)
     (16, 2, 256, 16, 9000, 0, True, True, 0, 0.0),       # 4 row groups (2R <= G behind >= 8k keys)
-    (40, 8, 128, 12, 17000, 3, False, False, 0, 0.0),    # 2 row groups at hd 128 behind >= 16k, f32 q/o
-    (64, 8, 128, 8, 12000, 0, True, True, 0, 0.0),       # 2R <= G = 8 behind 8k-16k keys
+    (40, 8, 128, 12, 17000, 3, False, False, 0, 0.0),    # 2 row groups at hd 128 behind >= 16k: packed, f32 q/o
+    (64, 8, 128, 8, 12000, 0, True, True, 0, 0.0),       # 2R <= G = 8 behind 8k-16k keys: packed
+    (16, 2, 256, 8, 17000, 0, False, False, 0, 0.0),     # 2 row groups that cannot pack: decode kernel, f32 q/o
     (48, 8, 128, 16, 9000, 0, True, True, 0, 0.0),       # R = 3, 2R <= G: packed rather than the decode kernel
     (16, 2, 256, 12, 20000, 0, True, False, 300, 20.0),  # window + softcap on that path
     # chunks of <= 128 queries behind >= 16k keys with packed (query, head-in-group) rows

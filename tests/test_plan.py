@@ -54,20 +54,22 @@ def test_bench_shapes(shape, want):
     ((16, 2, 256, 16, 9000), "decode"),               # R = 4
     ((16, 2, 256, 16, 8000), "prefill"),              # below 8k keys
     ((16, 2, 256, 20, 9000), "prefill"),              # R = 5: 2R > G, and below 16k
-    # behind >= 16k keys: R < G, and R <= 2 or no packed grid that fills the chip
-    ((16, 2, 256, 8, 17000), "decode"),               # R = 2
+    # behind >= 16k keys: R < G and no packed grid that fills the chip
+    ((16, 2, 256, 8, 17000), "decode"),               # R = 2, too few packed blocks
     ((16, 2, 256, 16, 17000), "decode"),              # R = 4: one packed block per kv head, too small a grid
     ((16, 2, 256, 24, 17000), "prefill"),             # R = 6 < 8, but 4 packed blocks fill the grid
     ((16, 2, 256, 32, 17000), "prefill"),             # R = 8 = G
     ((24, 4, 192, 24, 32768), "prefill"),             # R = 5 < 6, packed
     ((8, 1, 128, 16, 32768), "decode"),               # R = 4, one kv head: packing cannot fill the grid
-    ((40, 8, 128, 12, 17000), "decode"),              # R = 2 at head dim 128
+    ((40, 8, 128, 12, 17000), "prefill"),             # R = 2 at head dim 128: packed
+    ((16, 4, 128, 16, 32768), "prefill"),             # R = 2, G = 4: packed
     ((40, 8, 128, 24, 17000), "prefill"),             # R = 4 at head dim 128: packed rows
     ((64, 8, 128, 16, 32768), "prefill"),             # R = 4 < G = 8 at head dim 128: packed rows
     ((40, 8, 128, 32, 17000), "prefill"),             # R = 5 = G
     ((16, 8, 128, 24, 32768), "prefill"),             # R = 2 = G: nothing shared
-    # 2R <= G behind 8k-16k keys, again R <= 2 or no packed grid
-    ((64, 8, 128, 8, 12000), "decode"),               # R = 2
+    # 2R <= G behind 8k-16k keys, again without a packed grid
+    ((64, 8, 128, 8, 12000), "prefill"),              # R = 2: packed
+    ((64, 8, 128, 4, 12000), "decode"),               # one group
     ((64, 8, 128, 16, 12000), "prefill"),             # R = 4: packed
     ((16, 2, 256, 16, 9000), "decode"),               # R = 4: too few packed blocks
     ((64, 8, 128, 20, 12000), "prefill"),             # 2R = 10 > 8
