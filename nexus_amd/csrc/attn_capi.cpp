@@ -237,7 +237,20 @@ PrefillPlan prefill_plan_for(const nexus_attn_desc* d, bool pack)
     const long long b1 = query_blocks(d, nxa::prefill_wide_rows(1), pack), cus = device_cus();
     const bool ks2 = b1 <= cus || (b1 < 2 * cus && d->q_base_pos < d->n_query);
     p.ks = ks2 && d->head_dim <= 128 ? 2 : 1;
-    p.splits = prefill_splits(d, query_blocks(d, nxa::prefill_wide_rows(p.ks), pack));
+    const long long b = query_blocks(d, nxa::prefill_wide_rows(p.ks), pack);
+    p.splits = prefill_splits(d, b);
+    // Behind a cache of >= 8k keys at least as long as the chunk, 128-row blocks (K/V tiles shared
+    // by four row waves) in key splits beat 64-row ones when they pad no more rows and their
+    // split grid is as large (40q/8kv hd 128: 512 queries over 16k 215 -> 180 us, 200-384
+    // queries over 16-32k 7% faster; with more padding, 160 queries, or a smaller grid, 512
+    // queries over 8k with 64 q heads, 10-12% slower).
+    if (p.ks == 2 && d->q_base_pos >= d->n_query && d->q_base_pos >= 8192 && b == 2 * b1) {
+        const int s1 = prefill_splits(d, b1);
+        if ((long long)s1 * b1 >= (long long)p.splits * b) {
+            p.ks = 1;
+            p.splits = s1;
+        }
+    }
     return p;
 }
 

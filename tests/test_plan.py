@@ -130,8 +130,10 @@ def _plain_wgs(hq, hkv, hd, nq, base):
     ((16, 2, 256, 1024, 1024), P(128, 2, 256)),       # the engine's 1024-token tile at hd 256
     ((8, 2, 128, 256, 3000), P(64, 8, 256)),          # short chunk over a longer cache: key splits
     ((4, 4, 128, 64, 32768), P(64, 64, 256)),         # 4 blocks behind 32k keys: 64 splits
-    ((40, 8, 128, 256, 32768), P(64, 3, 480)),        # 160 blocks: split toward two per CU
-    ((32, 8, 128, 256, 16384), P(64, 4, 512)),        # 128 blocks
+    ((40, 8, 128, 256, 32768), P(128, 6, 480)),       # behind a long cache: 80 128-row blocks in 6 splits
+    ((40, 8, 128, 160, 32768), P(64, 4, 480)),        # ... unless 128-row blocks pad more rows
+    ((32, 8, 128, 256, 16384), P(128, 8, 512)),       # 64 128-row blocks
+    ((64, 8, 128, 512, 8192), P(64, 1, 512)),         # ... or give a smaller grid
     ((40, 8, 128, 64, 32768), P(64, 12, 480)),        # 40 blocks, 43 tiles per split at two per CU
     ((40, 8, 128, 24, 9000), P(64, 16, 256, True)),   # 16 packed blocks, too few tiles for two per CU
     ((16, 2, 256, 32, 32768), P(128, 64, 256, True)), # 4 packed blocks, 64 splits
