@@ -240,13 +240,15 @@ PrefillPlan prefill_plan_for(const nexus_attn_desc* d, bool pack)
     const long long b = query_blocks(d, nxa::prefill_wide_rows(p.ks), pack);
     p.splits = prefill_splits(d, b);
     // Behind a cache of >= 8k keys at least as long as the chunk, 128-row blocks (K/V tiles shared
-    // by four row waves) in key splits beat 64-row ones when they pad no more rows and their
-    // split grid is as large (40q/8kv hd 128: 512 queries over 16k 215 -> 180 us, 200-384
-    // queries over 16-32k 7% faster; with more padding, 160 queries, or a smaller grid, 512
-    // queries over 8k with 64 q heads, 10-12% slower).
+    // by four row waves) in key splits beat 64-row ones when they pad no more rows, their split
+    // grid is as large and each split keeps >= 16 key tiles (40q/8kv hd 128: 512 queries over 16k
+    // 215 -> 180 us, 200-384 queries over 16-32k 7% faster; with more padding, 160 queries, or a
+    // smaller grid, 512 queries over 8k with 64 q heads, 10-12% slower).
     if (p.ks == 2 && d->q_base_pos >= d->n_query && d->q_base_pos >= 8192 && b == 2 * b1) {
         const int s1 = prefill_splits(d, b1);
-        if ((long long)s1 * b1 >= (long long)p.splits * b) {
+        int kb, ke;
+        key_range(d, &kb, &ke);
+        if ((long long)s1 * b1 >= (long long)p.splits * b && 16LL * 64 * s1 <= ke - kb) {
             p.ks = 1;
             p.splits = s1;
         }
