@@ -204,7 +204,7 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // 1024 after 2048/3072/4096/7168 without the pairing 76/100/124/195 vs 80/107/136/223 us).  Head dims 192 and 256 have the 128-row form only: the two-key-group form does not fit
 // one wave per SIMD's registers.  Either grid splits the key range over workgroups by the rule
 // above.
-// Packed rows: a chunk of at most 128 queries with several q heads per kv head can have its
+// Packed rows: a chunk of at most 512 queries with several q heads per kv head can have its
 // blocks over the (query, head-in-group) pairs of each kv head instead of one padded block per q
 // head, so the group's heads share every K/V tile (read once per block, not once per q head) and
 // only the last block of a kv head is partly filled.  It pays behind long caches, where the
@@ -213,7 +213,9 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // workgroups of the unpacked one or of the CUs.  Measured on MI355X: 40q/8kv hd 128, 32/48/96
 // queries over 32k keys 90/92/160 -> 63/76/128 us, 24 over 9k 25.7 -> 18.1 us; 64q/8kv, 20
 // queries over 12k 39.3 -> 23.5 us, 40 over 32k (240 packed workgroups against 256) 129 -> 93
-// us; 24q/4kv hd 192, 48 queries over 12k 42.7 -> 34.7 us; as many blocks either way (40q/8kv, 64
+// us; 24q/4kv hd 192, 48 queries over 12k 42.7 -> 34.7 us; 129-512 queries, 16q/2kv hd 256, 160
+// over 32k 157 -> 114 us, 64q/8kv, 160 over 16k 130 -> 102 us, 40q/8kv, 200 over 32k 178 -> 153
+// us (packing was first limited to 128 queries); as many blocks either way (40q/8kv, 64
 // queries) or head dim 64 behind 9k keys: 1-7% slower packed; behind 4-6k keys within +-10%
 // either way; 16q/2kv hd 256, 32 queries over 8k packed into 64 workgroups instead of 256: 14%
 // slower.
@@ -264,7 +266,7 @@ long long prefill_plan_wgs(const nexus_attn_desc* d, const PrefillPlan& p)
 PrefillPlan prefill_plan(const nexus_attn_desc* d)
 {
     const PrefillPlan plain = prefill_plan_for(d, false);
-    if (d->n_query > 128 || d->n_q_heads == d->n_kv_heads || d->n_ctx < (d->head_dim >= 128 ? 8192 : 16384))
+    if (d->n_query > 512 || d->n_q_heads == d->n_kv_heads || d->n_ctx < (d->head_dim >= 128 ? 8192 : 16384))
         return plain;
     const PrefillPlan packed = prefill_plan_for(d, true);
     // packing must save K/V reads (fewer blocks) and keep the grid at 3/4 of the plain one or of the CUs

@@ -95,7 +95,9 @@ def test_short_chunk_route(shape, kernel):
     ((32, 8, 64, 48, 9000), False),                   # head dim 64 below 16k keys
     ((40, 8, 128, 64, 9000), False),                  # 40 blocks either way
     ((16, 2, 256, 32, 8192), False),                  # packing lost there (64 workgroups for 256)
-    ((40, 8, 128, 160, 32768), False),                # more than 128 queries
+    ((40, 8, 128, 160, 32768), True),                 # 160 queries: 13 packed blocks per kv head against 15
+    ((40, 8, 128, 256, 32768), False),                # 256 queries: as many blocks either way
+    ((40, 8, 128, 600, 32768), False),                # more than 512 queries
     ((8, 8, 128, 64, 20000), False),                  # no GQA group to pack
 ])
 def test_packed_rows_rule(shape, packed):
@@ -131,7 +133,7 @@ def _plain_wgs(hq, hkv, hd, nq, base):
     ((8, 2, 128, 256, 3000), P(64, 8, 256)),          # short chunk over a longer cache: key splits
     ((4, 4, 128, 64, 32768), P(64, 64, 256)),         # 4 blocks behind 32k keys: 64 splits
     ((40, 8, 128, 256, 32768), P(128, 6, 480)),       # behind a long cache: 80 128-row blocks in 6 splits
-    ((40, 8, 128, 160, 32768), P(64, 4, 480)),        # ... unless 128-row blocks pad more rows
+    ((8, 8, 128, 160, 32768), P(64, 21, 504)),        # ... unless 128-row blocks pad more rows
     ((32, 8, 128, 256, 16384), P(128, 8, 512)),       # 64 128-row blocks
     ((64, 8, 128, 512, 8192), P(64, 1, 512)),         # ... or give a smaller grid
     ((40, 8, 128, 64, 32768), P(64, 12, 480)),        # 40 blocks, 43 tiles per split at two per CU
