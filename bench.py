@@ -56,6 +56,12 @@ CONFIGS = {
                        "40q/8kv, hd128"),
     "q35t3": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=1024, base=3072, n_ctx=4096, q="f16", o="f16",
                   desc="the engine's 1024-token prompt tile after 3072 cached tokens, 16q/2kv, hd256 (key splits)"),
+    # short chunks behind a long cache read more K/V than they compute on: timed with the K/V
+    # rotated past the Infinity Cache like the decode configs
+    "c64": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=64, base=32768, n_ctx=32832, q="f16", o="f16", kvrot=True,
+                desc="a 64-query chunk after 32768 cached tokens, 40q/8kv, hd128 (packed rows in key splits)"),
+    "q35s": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=160, base=32768, n_ctx=32928, q="f16", o="f16", kvrot=True,
+                 desc="a 160-query chunk after 32768 cached tokens, 16q/2kv, hd256 (packed rows in key splits)"),
     "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
                  desc="MTP verify 4 drafts at 32768 cached tokens, 16q/2kv, hd256, causal among drafts"),
 }
@@ -105,7 +111,8 @@ def measure(name: str, steps: int, warmup: int, graph: bool = False, rotate: boo
     q = torch.randn(c["nq"], c["hq"], c["hd"], generator=g, device=dev).to(qdt)
     kv_bytes = 2 * c["hkv"] * c["n_ctx"] * c["hd"] * 2
     # memory-bound configs rotate over distinct K/V copies so reads come from HBM
-    n_sets = 1 if c["kind"] == "prefill" or not rotate else max(2, min(64, -(-2 * MALL_BYTES // kv_bytes)))
+    n_sets = 1 if (c["kind"] == "prefill" and not c.get("kvrot")) or not rotate else \
+        max(2, min(64, -(-2 * MALL_BYTES // kv_bytes)))
     kvs = []
     for _ in range(n_sets):
         k = torch.randn(c["hkv"], c["n_ctx"], c["hd"], generator=g, device=dev).half()
@@ -598,6 +605,8 @@ def main() -> int:
     extra["cfg2q32"] = measure("cfg2q32", args.steps, args.warmup, check=True)
     extra["tile3"] = measure("tile3", args.steps, args.warmup, check=True)
     extra["q35t3"] = measure("q35t3", args.steps, args.warmup, check=True)
+    extra["c64"] = measure("c64", args.steps, args.warmup, check=True)
+    extra["q35s"] = measure("q35s", args.steps, args.warmup, check=True)
     extra["cap2"] = measure("cap2", args.steps, args.warmup, check=True)
     extra["swa3"] = measure("swa3", max(5, args.steps // 5), args.warmup, check=True)
     extra["decode_layer"] = measure_decode_layer(args.steps, args.warmup)
