@@ -201,9 +201,9 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
 // MI355X with the CU pairing of pair_rotate, 40 q heads: 1024 queries cold 29.7 -> 25.4 us,
 // 36q/4kv 27.6 -> 21.4 us; from a cache as long as the chunk on, 128-row blocks are faster: 40
 // q heads, 1024 after 1024 51.1 vs 53.3 us, 48 q heads 52.3 vs 56.4, head dim 64 31.0 vs 36.6;
-// 1024 after 2048/3072/4096/7168 without the pairing 76/100/124/195 vs 80/107/136/223 us).  Head dims 192 and 256 have the 128-row form only: the two-key-group form does not fit
-// one wave per SIMD's registers.  Either grid splits the key range over workgroups by the rule
-// above.
+// 1024 after 2048/3072/4096/7168 without the pairing 76/100/124/195 vs 80/107/136/223 us).
+// Head dims 192 and 256 have the 128-row form only: the two-key-group form does not fit one wave
+// per SIMD's registers.  Either grid splits the key range over workgroups by the rule above.
 // Packed rows: a chunk of at most 512 queries with several q heads per kv head can have its
 // blocks over the (query, head-in-group) pairs of each kv head instead of one padded block per q
 // head, so the group's heads share every K/V tile (read once per block, not once per q head) and
