@@ -171,11 +171,12 @@ size_t prefill_split_ws_bytes(const nexus_attn_desc* d, int splits)
 // CU stays whole (320 pipelined workgroups of 64 queries x 40 heads in 2 splits took 96 us
 // against 62 unsplit).  Below that the key range is split so the grid reaches about one
 // workgroup per CU, or two at head dims <= 128 (two resident per CU; a workgroup alone on its CU
-// runs one wave per SIMD) while each split keeps >= 16 key tiles of 64; always >= 4 tiles per
+// runs one wave per SIMD) while each split keeps >= 12 key tiles of 64; always >= 4 tiles per
 // split and at most 64 splits.  Measured on MI355X: 40q/8kv hd 128, 200/256 queries over 32k
 // keys in 160 workgroups 432/427 us, split three ways 192/204 us; 32q/8kv, 256 over 16k (128
 // workgroups) 187 -> 90 us; 32/48/64 queries over 32k at one workgroup per CU 61/75/89 us, at two
-// 48/54/62 us; 24 over 9k (9 tiles per split at one per CU) 18 us, at two 24 us; 16q/2kv hd 256
+// 48/54/62 us, 64 over 12k (16 tiles per split at two) 36 -> 33 us; 24 over 9k (4 tiles per split
+// at two) 18 -> 24 us, 64 over 9k (12 tiles) 27.3 -> 27.7 us; 16q/2kv hd 256
 // behind 32k keys, 32/48 queries at most 16 splits 76/80 us, 64 splits 43/52 us; 24q/4kv hd 192,
 // 32 queries 93 -> 49 us; 4-head MHA, 64 queries 34 -> 21 us.
 int prefill_splits(const nexus_attn_desc* d, long long base)
@@ -186,8 +187,8 @@ int prefill_splits(const nexus_attn_desc* d, long long base)
     key_range(d, &kb, &ke);
     const long long tiles = (ke - kb + 63) / 64;
     long long s = cus / base;                                  // about one workgroup per CU
-    if (nxa::decode_wg_per_cu(d->head_dim) == 2 && tiles * base >= 16LL * 2 * cus)
-        s = 2 * cus / base;                                    // two, while splits keep >= 16 tiles
+    if (nxa::decode_wg_per_cu(d->head_dim) == 2 && tiles * base >= 12LL * 2 * cus)
+        s = 2 * cus / base;                                    // two, while splits keep >= 12 tiles
     if (s > tiles / 4) s = tiles / 4;
     if (s > 64) s = 64;
     return s < 1 ? 1 : (int)s;

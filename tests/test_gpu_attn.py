@@ -128,6 +128,7 @@ PREFILL_CASES = [
     (4, 4, 128, 64, 20000, 0, False, False, 0, 0.0),     # MHA, 4 blocks in 64 key splits, f32 q/o
     (40, 8, 128, 200, 12000, 0, True, True, 0, 0.0),     # 200 queries behind 12k keys, packed
     (16, 2, 256, 160, 17000, 0, True, False, 0, 0.0),    # 160 queries packed at hd 256
+    (32, 8, 64, 24, 17000, 0, True, True, 0, 0.0),       # packed at hd 64 behind >= 16k keys
     (8, 1, 128, 32, 20000, 0, True, False, 0, 0.0),      # one kv head: packed, 64 splits
     (24, 4, 192, 16, 20000, 0, True, True, 0, 0.0),      # R = 3 < G = 6: packed rather than the decode kernel
     (8, 1, 256, 16, 20000, 0, False, False, 0, 0.0),     # R = 4 < G = 8 that cannot pack: decode kernel
