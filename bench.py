@@ -59,7 +59,7 @@ CONFIGS = {
     # short chunks behind a long cache read more K/V than they compute on: timed with the K/V
     # rotated past the Infinity Cache like the decode configs
     "c64": dict(kind="prefill", hq=40, hkv=8, hd=128, nq=64, base=32768, n_ctx=32832, q="f16", o="f16", kvrot=True,
-                desc="a 64-query chunk after 32768 cached tokens, 40q/8kv, hd128 (packed rows in key splits)"),
+                desc="a 64-query chunk after 32768 cached tokens, 40q/8kv, hd128 (64-row blocks in key splits)"),
     "q35s": dict(kind="prefill", hq=16, hkv=2, hd=256, nq=160, base=32768, n_ctx=32928, q="f16", o="f16", kvrot=True,
                  desc="a 160-query chunk after 32768 cached tokens, 16q/2kv, hd256 (packed rows in key splits)"),
     "cfg5": dict(kind="verify", hq=16, hkv=2, hd=256, nq=4, base=32768, n_ctx=32772, q="f32", o="f32", splits=0,
